@@ -1,0 +1,302 @@
+"""ctypes binding of ``libfat_hip.so`` (the C ABI declared in ``include/fat_abi.h``).
+
+This is the MI355X replacement of the reference's lazy nvcc build
+(``flashattn_tile/native.py:17-51``): the HIP library is compiled ahead of
+time (``flashattntile_amd/csrc/build.py``) and loaded here once, under a lock.
+Nothing here falls back to a CPU path: if the library cannot be loaded every
+entry point raises ``RuntimeError`` naming the reason.
+
+Tensors cross the boundary as raw device pointers, element strides and sizes;
+kernels are enqueued on torch's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
+ABI_VERSION = 1
+
+# enum fat_dtype
+DT_F16 = 0
+DT_BF16 = 1
+DT_I8 = 2
+DT_FP8E4M3 = 3
+
+EXPORTED_SYMBOLS = (
+    "fat_abi_version",
+    "fat_last_error",
+    "fat_paged_decode_workspace_bytes",
+    "fat_paged_decode",
+    "fat_prefill_workspace_bytes",
+    "fat_prefill_varlen",
+)
+
+_c_i64 = ctypes.c_int64
+_c_i32 = ctypes.c_int32
+_c_vp = ctypes.c_void_p
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``fat_decode_args``."""
+
+    _fields_ = [
+        ("q", _c_vp),
+        ("k_cache", _c_vp),
+        ("v_cache", _c_vp),
+        ("k_scale", _c_vp),
+        ("v_scale", _c_vp),
+        ("page_table", _c_vp),
+        ("seq_lens", _c_vp),
+        ("out", _c_vp),
+        ("workspace", _c_vp),
+        ("q_stride_b", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("k_stride_page", _c_i64),
+        ("k_stride_slot", _c_i64),
+        ("k_stride_head", _c_i64),
+        ("v_stride_page", _c_i64),
+        ("v_stride_slot", _c_i64),
+        ("v_stride_head", _c_i64),
+        ("scale_stride_page", _c_i64),
+        ("scale_stride_head", _c_i64),
+        ("page_table_stride", _c_i64),
+        ("out_stride_b", _c_i64),
+        ("out_stride_h", _c_i64),
+        ("batch", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("page_size", _c_i32),
+        ("num_pages", _c_i32),
+        ("max_pages", _c_i32),
+        ("split_k", _c_i32),
+        ("waves_per_group", _c_i32),
+        ("q_dtype", _c_i32),
+        ("kv_dtype", _c_i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ``fat_prefill_args``."""
+
+    _fields_ = [
+        ("q", _c_vp),
+        ("k", _c_vp),
+        ("v", _c_vp),
+        ("cu_seqlens_q", _c_vp),
+        ("cu_seqlens_k", _c_vp),
+        ("out", _c_vp),
+        ("workspace", _c_vp),
+        ("q_stride_t", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("k_stride_t", _c_i64),
+        ("k_stride_h", _c_i64),
+        ("v_stride_t", _c_i64),
+        ("v_stride_h", _c_i64),
+        ("out_stride_t", _c_i64),
+        ("out_stride_h", _c_i64),
+        ("batch", _c_i32),
+        ("total_q", _c_i32),
+        ("total_k", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("max_seqlen_q", _c_i32),
+        ("max_seqlen_k", _c_i32),
+        ("causal", _c_i32),
+        ("dtype", _c_i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+_ERROR: str | None = None
+_TRIED = False
+
+
+def _load() -> None:
+    global _LIB, _ERROR, _TRIED
+    with _LOCK:
+        if _TRIED:
+            return
+        _TRIED = True
+        path = Path(os.environ.get("FAT_HIP_LIB", str(LIB_PATH)))
+        if not path.exists():
+            _ERROR = f"{path} not found; build it with `python -m flashattntile_amd.csrc.build`"
+            return
+        try:
+            # torch's HIP runtime is already loaded (import torch above), so the
+            # library binds to the same libamdhip64 instance.
+            lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
+        except OSError as exc:
+            _ERROR = f"cannot load {path}: {exc}"
+            return
+        lib.fat_abi_version.restype = ctypes.c_int
+        lib.fat_last_error.restype = ctypes.c_char_p
+        lib.fat_paged_decode_workspace_bytes.restype = ctypes.c_size_t
+        lib.fat_paged_decode_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32, _c_i32]
+        lib.fat_paged_decode.restype = ctypes.c_int
+        lib.fat_paged_decode.argtypes = [ctypes.POINTER(DecodeArgs), _c_vp]
+        lib.fat_prefill_workspace_bytes.restype = ctypes.c_size_t
+        lib.fat_prefill_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32]
+        lib.fat_prefill_varlen.restype = ctypes.c_int
+        lib.fat_prefill_varlen.argtypes = [ctypes.POINTER(PrefillArgs), _c_vp]
+        version = lib.fat_abi_version()
+        if version != ABI_VERSION:
+            _ERROR = f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it"
+            return
+        _LIB = lib
+
+
+def is_loaded() -> bool:
+    """Load the library once; True if it is usable."""
+    _load()
+    return _LIB is not None
+
+
+def load_error() -> str:
+    """Why the library is unusable ('' when it loaded)."""
+    _load()
+    return "" if _LIB is not None else (_ERROR or "libfat_hip.so not loaded")
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError (no fallback) when unavailable."""
+    _load()
+    if _LIB is None:
+        raise RuntimeError(f"HIP kernel library unavailable: {_ERROR}")
+    return _LIB
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return DT_F16
+    if dtype == torch.bfloat16:
+        return DT_BF16
+    if dtype == torch.int8:
+        return DT_I8
+    if dtype == getattr(torch, "float8_e4m3fn", None):
+        return DT_FP8E4M3
+    raise TypeError(f"no HIP kernel element type for {dtype}")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().fat_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def current_stream_handle(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, split_k: int) -> int:
+    return int(lib().fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k))
+
+
+def prefill_workspace_bytes(total_k: int, num_kv_heads: int, head_dim: int) -> int:
+    return int(lib().fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim))
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    out: torch.Tensor,
+    page_size: int,
+    softmax_scale: float,
+    split_k: int,
+    workspace: torch.Tensor | None = None,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    stream: int | None = None,
+    waves_per_group: int = 0,
+) -> None:
+    """Enqueue ``fat_paged_decode`` for already-validated device tensors."""
+    a = DecodeArgs()
+    a.q = _ptr(q)
+    a.k_cache = _ptr(k_cache)
+    a.v_cache = _ptr(v_cache)
+    a.k_scale = _ptr(k_scale)
+    a.v_scale = _ptr(v_scale)
+    a.page_table = _ptr(page_table)
+    a.seq_lens = _ptr(seq_lens)
+    a.out = _ptr(out)
+    a.workspace = _ptr(workspace)
+    a.q_stride_b, a.q_stride_h = q.stride(0), q.stride(1)
+    a.k_stride_page, a.k_stride_slot, a.k_stride_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_stride_page, a.v_stride_slot, a.v_stride_head = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    if k_scale is not None:
+        a.scale_stride_page, a.scale_stride_head = k_scale.stride(0), k_scale.stride(1)
+    a.page_table_stride = page_table.stride(0)
+    a.out_stride_b, a.out_stride_h = out.stride(0), out.stride(1)
+    a.batch = q.shape[0]
+    a.num_heads = q.shape[1]
+    a.num_kv_heads = k_cache.shape[2]
+    a.head_dim = q.shape[2]
+    a.page_size = int(page_size)
+    a.num_pages = k_cache.shape[0]
+    a.max_pages = page_table.shape[1]
+    a.split_k = int(split_k)
+    a.waves_per_group = int(waves_per_group)
+    a.q_dtype = dtype_code(q.dtype)
+    a.kv_dtype = dtype_code(k_cache.dtype)
+    a.softmax_scale = float(softmax_scale)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
+
+
+def prefill_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    out: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    causal: bool,
+    softmax_scale: float,
+    workspace: torch.Tensor | None = None,
+    stream: int | None = None,
+) -> None:
+    """Enqueue ``fat_prefill_varlen`` for already-validated device tensors."""
+    a = PrefillArgs()
+    a.q = _ptr(q)
+    a.k = _ptr(k)
+    a.v = _ptr(v)
+    a.cu_seqlens_q = _ptr(cu_seqlens_q)
+    a.cu_seqlens_k = _ptr(cu_seqlens_k)
+    a.out = _ptr(out)
+    a.workspace = _ptr(workspace)
+    a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1)
+    a.k_stride_t, a.k_stride_h = k.stride(0), k.stride(1)
+    a.v_stride_t, a.v_stride_h = v.stride(0), v.stride(1)
+    a.out_stride_t, a.out_stride_h = out.stride(0), out.stride(1)
+    a.batch = cu_seqlens_q.shape[0] - 1
+    a.total_q = q.shape[0]
+    a.total_k = k.shape[0]
+    a.num_heads = q.shape[1]
+    a.num_kv_heads = k.shape[1]
+    a.head_dim = q.shape[2]
+    a.max_seqlen_q = int(max_seqlen_q)
+    a.max_seqlen_k = int(max_seqlen_k)
+    a.causal = 1 if causal else 0
+    a.dtype = dtype_code(q.dtype)
+    a.softmax_scale = float(softmax_scale)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")

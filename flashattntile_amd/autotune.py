@@ -1,0 +1,122 @@
+"""Analytic work accounting and the MI355X launch heuristics.
+
+The FLOP and byte formulas are the reference's roofline numerators
+(``flashattn_tile/autotune.py:31-106``) so achieved-throughput figures are
+comparable:
+
+* ``flops = 4 * B * H * D * pairs`` (QK^T and PV, 2 FLOP per MAC; softmax
+  excluded), ``pairs = q*kv`` or, causal bottom-right,
+  ``q*(kv - q) + q*(q + 1)/2``;
+* decode bytes = q + K + V + o; prefill bytes = q + k + v + o.
+
+The Triton knob search of the reference (BLOCK_M/N, num_warps, num_stages and
+its JSON store) has no meaning for the HIP kernels.  What does matter on
+MI355X is how many workgroups a decode launch puts on the 256 CUs, so the
+split-K count is derived from the shape and the CU count instead
+(:func:`decode_split_k`).
+"""
+
+from __future__ import annotations
+
+import math
+
+__all__ = [
+    "flops_attention",
+    "flops_attention_varlen",
+    "bytes_attention",
+    "bytes_decode_paged",
+    "arithmetic_intensity",
+    "decode_split_k",
+    "MI355X_CUS",
+]
+
+MI355X_CUS = 256
+
+
+def _causal_pairs(q_len: int, kv_len: int) -> int:
+    """Query/key pairs visible under bottom-right causal alignment."""
+    if q_len <= 0 or kv_len <= 0:
+        return 0
+    if kv_len < q_len:
+        raise ValueError("causal accounting requires kv_len >= q_len")
+    return q_len * (kv_len - q_len) + q_len * (q_len + 1) // 2
+
+
+def flops_attention(num_heads: int, head_dim: int, q_len: int, kv_len: int,
+                    causal: bool = False, batch: int = 1) -> int:
+    """``4 * batch * H * D * pairs`` (``autotune.py:40-55``)."""
+    pairs = _causal_pairs(q_len, kv_len) if causal else q_len * kv_len
+    return int(4 * batch * num_heads * head_dim * pairs)
+
+
+def flops_attention_varlen(num_heads: int, head_dim: int, q_lens, kv_lens, causal: bool = False) -> int:
+    """Sum of :func:`flops_attention` over a ragged batch (``autotune.py:58-73``)."""
+    if len(q_lens) != len(kv_lens):
+        raise ValueError("q_lens and kv_lens must have the same length")
+    return int(sum(flops_attention(num_heads, head_dim, int(q), int(k), causal=causal)
+                   for q, k in zip(q_lens, kv_lens)))
+
+
+def bytes_attention(mode: str, batch: int, q_len: int, kv_len: int, num_heads: int,
+                    num_kv_heads: int, head_dim: int, elem_bytes: int = 2) -> int:
+    """HBM bytes of the fused kernel: q + K + V + o (``autotune.py:76-106``)."""
+    if mode == "decode":
+        if q_len != 1:
+            raise ValueError("decode accounting assumes q_len == 1")
+        q_bytes = batch * num_heads * head_dim * elem_bytes
+        kv_bytes = batch * kv_len * num_kv_heads * head_dim * 2 * elem_bytes
+        return int(2 * q_bytes + kv_bytes)
+    if mode == "prefill":
+        q_bytes = batch * q_len * num_heads * head_dim * elem_bytes
+        kv_bytes = batch * kv_len * num_kv_heads * head_dim * 2 * elem_bytes
+        return int(2 * q_bytes + kv_bytes)
+    raise ValueError(f"unknown mode {mode!r}")
+
+
+def bytes_decode_paged(seq_lens, num_heads: int, num_kv_heads: int, head_dim: int,
+                       q_elem_bytes: int = 2, kv_elem_bytes: int = 2, page_size: int | None = None,
+                       quantized: bool = False) -> int:
+    """Decode bytes for a ragged batch: q + o + sum_b ctx_b * (K + V).
+
+    For a quantised cache the fp32 scales of every touched (page, KV head) are
+    added (2 * 4 bytes each), the scale term of ``kv_bytes_per_token``
+    (``quant.py:205-208``).  The page table is excluded, as in the reference.
+    """
+    lens = [int(x) for x in seq_lens]
+    batch = len(lens)
+    qo = 2 * batch * num_heads * head_dim * q_elem_bytes
+    kv = sum(lens) * num_kv_heads * head_dim * 2 * kv_elem_bytes
+    scales = 0
+    if quantized:
+        if page_size is None:
+            raise ValueError("quantized accounting needs page_size")
+        pages = sum(math.ceil(n / page_size) for n in lens)
+        scales = pages * num_kv_heads * 2 * 4
+    return int(qo + kv + scales)
+
+
+def arithmetic_intensity(flops: float, nbytes: float) -> float:
+    if nbytes <= 0:
+        return float("inf")
+    return float(flops) / float(nbytes)
+
+
+def decode_split_k(batch: int, num_heads: int, num_kv_heads: int, max_pages: int,
+                   num_cus: int = MI355X_CUS, waves_per_cu: int = 12) -> int:
+    """Split-K partitions for a decode launch on MI355X.
+
+    One workgroup (4 waves) handles one GQA group of up to 8 query heads for
+    one partition, so a launch has ``batch * groups * split`` workgroups.  The
+    heuristic asks for enough workgroups to keep ``waves_per_cu`` waves
+    resident on every CU (the kernel runs 3 waves per SIMD), never more
+    partitions than the page table has pages, and at most 64 (the reference's
+    limit, ``decode.py:492-495``).  It needs only host-known sizes, so it never
+    synchronises with the device.
+    """
+    group = max(1, num_heads // max(1, num_kv_heads))
+    heads_per_wg = 8 if group >= 8 else 4
+    groups = num_kv_heads * math.ceil(group / heads_per_wg)
+    base = max(1, batch * groups)
+    target_wgs = num_cus * waves_per_cu // 4
+    split = math.ceil(target_wgs / base)
+    return int(max(1, min(split, 64, max(1, max_pages))))

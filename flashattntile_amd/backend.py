@@ -1,0 +1,129 @@
+"""vLLM-shaped attention backend routing prefill and decode to the HIP kernels.
+
+Mirror of ``flashattn_tile/backend.py:37-175`` (same class, method names,
+metadata fields and errors):
+
+* ``get_name()`` -> ``"flashattn_tile"``;
+* ``get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_dim)`` ->
+  ``(2, num_blocks, block_size, num_kv_heads, head_dim)``;
+* ``forward(query, kv_cache, attn_metadata)`` runs causal varlen prefill when
+  ``attn_metadata.is_prefill`` and paged decode otherwise.
+
+An int8/fp8 :class:`PagedKVCache` is routed to the quantised decode kernel
+when ``attn_metadata.kv_scales`` carries its scales (an extension field; the
+reference backend had no quantised route).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
+from .kernels.prefill import prefill_attention
+from .paging import PagedKVCache, allocate
+
+KV_CACHE_NDIM = 4
+
+
+@dataclass
+class AttentionMetadata:
+    """Per-step metadata for :meth:`FlashAttnTileBackend.forward`."""
+
+    page_table: torch.Tensor | None = None
+    seq_lens: torch.Tensor | None = None
+    cu_seqlens_q: torch.Tensor | None = None
+    cu_seqlens_k: torch.Tensor | None = None
+    is_prefill: bool = False
+    max_seqlen_q: int | None = None
+    max_seqlen_k: int | None = None
+    # Packed K/V of the tokens being prefilled ([total_k, num_kv_heads, head_dim]).
+    k: torch.Tensor | None = None
+    v: torch.Tensor | None = None
+    softmax_scale: float | None = None
+    # Scales of a quantised cache (QuantScales or {"k": ..., "v": ...}).
+    kv_scales: object | None = None
+
+
+def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int,
+                       head_dim: int) -> tuple[int, int, int, int, int]:
+    """vLLM-style cache shape ``(2, blocks, block_size, kv_heads, head_dim)``."""
+    return (2, int(num_blocks), int(block_size), int(num_kv_heads), int(head_dim))
+
+
+class FlashAttnTileBackend:
+    """Paged attention backend for the MI355X kernels."""
+
+    def __init__(self, num_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                 dtype: torch.dtype | None = None, device: torch.device | str | None = None) -> None:
+        if num_heads % num_kv_heads != 0:
+            raise ValueError(f"num_heads {num_heads} must be divisible by num_kv_heads {num_kv_heads}")
+        if page_size <= 0:
+            raise ValueError("page_size must be positive")
+        self.num_heads = int(num_heads)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = int(head_dim)
+        self.page_size = int(page_size)
+        self.dtype = dtype
+        self.device = device
+
+    def get_name(self) -> str:
+        return "flashattn_tile"
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int,
+                           head_dim: int) -> tuple[int, int, int, int, int]:
+        return get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_dim)
+
+    @staticmethod
+    def get_kv_cache_shape_per_tensor(num_blocks: int, block_size: int, num_kv_heads: int,
+                                      head_dim: int) -> tuple[int, int, int, int]:
+        return (int(num_blocks), int(block_size), int(num_kv_heads), int(head_dim))
+
+    def allocate_kv_cache(self, batch: int, max_seq_len: int, dtype: torch.dtype = torch.float16,
+                          device: torch.device | str = "cuda") -> PagedKVCache:
+        return allocate(batch=batch, max_seq_len=max_seq_len, num_kv_heads=self.num_kv_heads,
+                        head_dim=self.head_dim, page_size=self.page_size, dtype=dtype, device=device)
+
+    def _resolve_cache(self, kv_cache: PagedKVCache, meta: AttentionMetadata) -> PagedKVCache:
+        if meta.page_table is None and meta.seq_lens is None:
+            return kv_cache
+        return PagedKVCache(
+            k_cache=kv_cache.k_cache,
+            v_cache=kv_cache.v_cache,
+            page_table=kv_cache.page_table if meta.page_table is None else meta.page_table,
+            seq_lens=kv_cache.seq_lens if meta.seq_lens is None else meta.seq_lens,
+            page_size=kv_cache.page_size,
+        )
+
+    def forward(self, query: torch.Tensor, kv_cache: PagedKVCache, attn_metadata: AttentionMetadata) -> torch.Tensor:
+        """Route ``query`` through prefill or paged decode (``backend.py:132-175``)."""
+        if not isinstance(kv_cache, PagedKVCache):
+            raise TypeError("kv_cache must be a PagedKVCache")
+        meta = attn_metadata
+        cache = self._resolve_cache(kv_cache, meta)
+        if not meta.is_prefill and query.dim() == 4:
+            query = query.squeeze(1)
+        if query.dim() != 3:
+            raise ValueError(f"query must be 3-D, got {tuple(query.shape)}")
+        if query.shape[1] != self.num_heads:
+            raise ValueError(f"query has {query.shape[1]} heads, backend expects {self.num_heads}")
+
+        if meta.is_prefill:
+            if meta.cu_seqlens_q is None or meta.cu_seqlens_k is None:
+                raise ValueError("prefill routing requires cu_seqlens_q and cu_seqlens_k")
+            max_q, max_k = meta.max_seqlen_q, meta.max_seqlen_k
+            if max_q is None:
+                max_q = int((meta.cu_seqlens_q[1:] - meta.cu_seqlens_q[:-1]).max())
+            if max_k is None:
+                max_k = int((meta.cu_seqlens_k[1:] - meta.cu_seqlens_k[:-1]).max())
+            if meta.k is None or meta.v is None:
+                raise ValueError("prefill routing requires attn_metadata.k and attn_metadata.v "
+                                 "(packed [total_k, num_kv_heads, head_dim])")
+            return prefill_attention(query, meta.k, meta.v, meta.cu_seqlens_q, meta.cu_seqlens_k,
+                                     int(max_q), int(max_k), causal=True, softmax_scale=meta.softmax_scale)
+
+        if meta.kv_scales is not None:
+            return paged_decode_attention_fp8(query, cache, meta.kv_scales, softmax_scale=meta.softmax_scale)
+        return paged_decode_attention(query, cache, softmax_scale=meta.softmax_scale)

@@ -1,0 +1,607 @@
+// decode.hip -- single-query paged decode for gfx950 (fp16/bf16/int8/fp8 K/V).
+//
+// Behaviour follows the FlashAttnTile decode path:
+//   flashattn_tile/kernels/decode.py:47-127   (_decode_paged_kernel)
+//   flashattn_tile/kernels/decode.py:223-356  (split kernel + LSE reduce)
+//   flashattn_tile/kernels/decode.py:359-447  (quantised K/V)
+// Design (MI355X-first, not a translation of the Triton programs):
+//   * one workgroup per (split, GQA head group, sequence); the HG query heads
+//     of a group share one KV head, so every K/V page is read from HBM once
+//     per group instead of once per query head;
+//   * a wave streams 16-token units; lane (r, c) owns row r of each 16-byte
+//     wide load and dims [c*EPL, c*EPL+EPL); K and V rows arrive as
+//     global_load_dwordx4, one unit ahead of the compute (register double
+//     buffer);
+//   * q.k partial sums are reduced across the LPR lanes of a row with a
+//     transposing DPP butterfly that leaves one (head, token) score per lane;
+//   * softmax state (running max m, sum l) is shared by the whole wave; the
+//     probabilities are broadcast to the PV lanes through a few bytes of LDS;
+//   * PV accumulates in fp32 (no rounding of p), matching the fp32 oracle;
+//   * int8/fp8 pages are dequantised in registers as
+//     round_to_q_dtype(float(x) * scale), the reference's own
+//     dequantise-then-attend semantics (flashattn_tile/quant.py:145-161);
+//   * with split_k > 1 each workgroup writes (acc, m, l) for its partition
+//     and a second kernel merges the partitions by log-sum-exp.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "fat_common.h"
+
+namespace fat {
+
+enum KvKind { KV_SAME = 0, KV_I8 = 1, KV_FP8 = 2 };
+
+struct DecodeParams {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  const float* ks;
+  const float* vs;
+  const int32_t* pt;
+  const int32_t* lens;
+  uint8_t* out;
+  float* ws_acc;  // [B, H, S, D]
+  float* ws_ml;   // [B, H, S, 2]  (m in log2 units, l)
+  int64_t q_sb, q_sh;
+  int64_t k_sp, k_ss, k_sh;
+  int64_t v_sp, v_ss, v_sh;
+  int64_t sc_sp, sc_sh;
+  int64_t pt_sb;
+  int64_t o_sb, o_sh;
+  int32_t H, Hkv, group, hg_per_kv;
+  int32_t P, log2P, num_pages, max_pages;
+  float scale_log2;  // softmax_scale * log2(e)
+};
+
+// Lane geometry for one 16-byte load per lane.
+template <int KV, int D>
+struct Geom {
+  static constexpr int kElemBytes = (KV == KV_SAME) ? 2 : 1;
+  static constexpr int kEpl = 16 / kElemBytes;  // elements per lane per row
+  static constexpr int kLpr = D / kEpl;         // lanes per row
+  static constexpr int kRpl = 64 / kLpr;        // rows per load
+  static constexpr int kNi = 16 / kRpl;         // loads per 16-token unit
+  static_assert(kLpr == 4 || kLpr == 8 || kLpr == 16, "unsupported head_dim / element size");
+};
+
+// One transposing butterfly step on lane bit BIT: NCUR values -> NCUR/2.
+template <int BIT, int NCUR>
+__device__ __forceinline__ void tr_step(float* x, bool up) {
+#pragma unroll
+  for (int j = 0; j < NCUR / 2; ++j) {
+    const float lo = x[j];
+    const float hi = x[j + NCUR / 2];
+    const float slo = lo + row_partner<BIT>(lo);
+    const float shi = hi + row_partner<BIT>(hi);
+    x[j] = up ? shi : slo;
+  }
+}
+
+// Sum N per-lane partials over the LPR lanes of a row; afterwards lane c
+// holds the full sums of values j = c * (N / LPR) + k, k < N / LPR.
+template <int LPR, int N>
+__device__ __forceinline__ void transpose_reduce(float* x, int c) {
+  static_assert(N >= LPR, "need at least one value per lane");
+  if constexpr (LPR >= 16) tr_step<8, N>(x, (c & 8) != 0);
+  if constexpr (LPR >= 8) tr_step<4, N * 8 / LPR>(x, (c & 4) != 0);
+  if constexpr (LPR >= 4) tr_step<2, N * 4 / LPR>(x, (c & 2) != 0);
+  tr_step<1, N * 2 / LPR>(x, (c & 1) != 0);
+}
+
+// Registers holding one unit's K/V rows (and per-load scales for 8-bit K/V).
+template <int NI>
+struct UnitRegs {
+  u32x4 k[NI];
+  u32x4 v[NI];
+  float ksc[NI];
+  float vsc[NI];
+};
+
+template <typename QT, int KV, int D, int HG, int NW>
+__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
+  using Gm = Geom<KV, D>;
+  constexpr int EPL = Gm::kEpl, LPR = Gm::kLpr, RPL = Gm::kRpl, NI = Gm::kNi;
+  constexpr int NV = NI * HG;       // per-lane partial scores before the reduction
+  constexpr int NPL = NV / LPR;     // scores per lane after it
+  constexpr int VPH = NPL < NI ? NPL : NI;  // scores per lane per head
+  constexpr int HPL = NPL / VPH;            // heads per lane
+  constexpr int LPH = NI / VPH;             // lanes per head inside a row
+  constexpr int QW = EPL / 2;               // q dwords per head per lane (packed pairs)
+  static_assert(HG % 4 == 0, "HG must be a multiple of 4");
+
+  __shared__ float s_p[NW][RPL][NV];
+  __shared__ float s_alpha[NW][HG];
+  __shared__ float s_red[NW][HG][D];
+  __shared__ float s_ml[NW][HG][2];
+
+  const int split = blockIdx.x;
+  const int S = gridDim.x;
+  const int y = blockIdx.y;
+  const int b = blockIdx.z;
+  const int sub = y % p.hg_per_kv;
+  const int kvh = y / p.hg_per_kv;
+  const int head0 = kvh * p.group + sub * HG;
+  const int nvalid = min(HG, p.group - sub * HG);
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane / LPR;
+  const int c = lane % LPR;
+
+  // Partition of this sequence's pages (decode.py:271-276 semantics).
+  int seq_len = p.lens[b];
+  seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
+  const int np = (seq_len + p.P - 1) >> p.log2P;
+  const int pps = (np + S - 1) / S;
+  const int pb = split * pps;
+  const int pe = min(np, pb + pps);
+  const int t_begin = pb << p.log2P;
+  const int t_end = min(seq_len, pe << p.log2P);
+  const int n_units = t_end > t_begin ? (t_end - t_begin + 15) >> 4 : 0;
+
+  // q for the HG heads, packed pairs of QT (padded heads reuse head0).
+  u32 qv[HG][QW];
+#pragma unroll
+  for (int g = 0; g < HG; ++g) {
+    const int h = head0 + (g < nvalid ? g : 0);
+    const u32x4* qp = reinterpret_cast<const u32x4*>(p.q + 2 * (b * p.q_sb + h * p.q_sh + c * EPL));
+#pragma unroll
+    for (int j = 0; j < QW / 4; ++j) {
+      const u32x4 t = qp[j];
+      qv[g][4 * j + 0] = t[0];
+      qv[g][4 * j + 1] = t[1];
+      qv[g][4 * j + 2] = t[2];
+      qv[g][4 * j + 3] = t[3];
+    }
+  }
+
+  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
+  const int64_t kv_head_off_k = (int64_t)kvh * p.k_sh + c * EPL;
+  const int64_t kv_head_off_v = (int64_t)kvh * p.v_sh + c * EPL;
+  constexpr int EB = Gm::kElemBytes;
+
+  auto fetch = [&](UnitRegs<NI>& R, int u) {
+    const int base = t_begin + (u << 4);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      int rs = base + i * RPL;
+      if (rs >= t_end) rs = (t_end - 1) & ~(RPL - 1);
+      int phys = ptrow[rs >> p.log2P];
+      phys = min(max(phys, 0), p.num_pages - 1);
+      const int tok = min(rs + r, t_end - 1);
+      const int slot = tok & (p.P - 1);
+      const uint8_t* kp = p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + kv_head_off_k);
+      const uint8_t* vp = p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + kv_head_off_v);
+      R.k[i] = *reinterpret_cast<const u32x4*>(kp);
+      R.v[i] = *reinterpret_cast<const u32x4*>(vp);
+      if constexpr (KV != KV_SAME) {
+        R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+        R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+      }
+    }
+  };
+
+  // Dequantise 16 bytes of 8-bit K/V into EPL/2 packed QT pairs:
+  // round_to_QT(float(x) * scale).
+  auto deq_pairs = [&](const u32x4& raw, float sc, u32* out) {
+    const float nb = -128.0f * sc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float f[4];
+      if constexpr (KV == KV_I8) {
+        i8x4_biased(raw[j], f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = __builtin_fmaf(f[e], sc, nb);
+      } else {
+        fp8x4(raw[j], f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = f[e] * sc;
+      }
+      out[2 * j + 0] = Pair<QT>::pack(f[0], f[1]);
+      out[2 * j + 1] = Pair<QT>::pack(f[2], f[3]);
+    }
+  };
+
+  float m_run[HPL], l_run[HPL];
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) {
+    m_run[hh] = -INFINITY;
+    l_run[hh] = 0.f;
+  }
+  float acc[HG][EPL];
+#pragma unroll
+  for (int g = 0; g < HG; ++g)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+
+  UnitRegs<NI> nxt;
+  if (w < n_units) fetch(nxt, w);
+
+  for (int u = w; u < n_units; u += NW) {
+    const UnitRegs<NI> cur = nxt;
+    if (u + NW < n_units) fetch(nxt, u + NW);
+    const int base = t_begin + (u << 4);
+
+    // ---- scores: partial q.k over this lane's EPL dims ----
+    float part[NV];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      u32 kw[QW];
+      if constexpr (KV == KV_SAME) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kw[j] = cur.k[i][j];
+      } else {
+        deq_pairs(cur.k[i], cur.ksc[i], kw);
+      }
+#pragma unroll
+      for (int g = 0; g < HG; ++g) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < QW; ++j) s = Pair<QT>::dot2(qv[g][j], kw[j], s);
+        part[g * NI + i] = s;
+      }
+    }
+    transpose_reduce<LPR, NV>(part, c);
+
+    // ---- online softmax (state shared by the wave, per head) ----
+    float pr[NPL];
+    float alpha[HPL];
+#pragma unroll
+    for (int hh = 0; hh < HPL; ++hh) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < VPH; ++v) {
+        const int k = hh * VPH + v;
+        const int j = c * NPL + k;
+        const int i = j % NI;
+        const bool valid = base + i * RPL + r < t_end;
+        const float s = valid ? part[k] * p.scale_log2 : -INFINITY;
+        pr[k] = s;
+        mx = fmaxf(mx, s);
+      }
+      mx = within_quad<OpMax, LPH>(mx);
+      mx = across_rows<OpMax, LPR>(mx);
+      const float m_new = fmaxf(m_run[hh], mx);
+      alpha[hh] = fast_exp2(m_run[hh] - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int v = 0; v < VPH; ++v) {
+        const int k = hh * VPH + v;
+        pr[k] = fast_exp2(pr[k] - m_new);
+        ps += pr[k];
+      }
+      l_run[hh] = l_run[hh] * alpha[hh] + ps;
+      m_run[hh] = m_new;
+    }
+
+    // ---- broadcast p (per row) and alpha (per wave) through LDS ----
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) s_p[w][r][c * NPL + k] = pr[k];
+    if (r == 0) {
+#pragma unroll
+      for (int hh = 0; hh < HPL; ++hh) {
+        const int j0 = c * NPL + hh * VPH;
+        if (j0 % NI == 0) s_alpha[w][j0 / NI] = alpha[hh];
+      }
+    }
+    wave_lds_fence();
+    float pv[NV];
+    float al[HG];
+#pragma unroll
+    for (int j = 0; j < NV; j += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(&s_p[w][r][j]);
+      pv[j] = t[0];
+      pv[j + 1] = t[1];
+      pv[j + 2] = t[2];
+      pv[j + 3] = t[3];
+    }
+#pragma unroll
+    for (int g = 0; g < HG; g += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(&s_alpha[w][g]);
+      al[g] = t[0];
+      al[g + 1] = t[1];
+      al[g + 2] = t[2];
+      al[g + 3] = t[3];
+    }
+    wave_lds_fence();
+
+    // ---- acc = acc * alpha + sum_i p_i * v_i (fp32) ----
+#pragma unroll
+    for (int g = 0; g < HG; ++g)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] *= al[g];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float vf[EPL];
+      u32 vw[QW];
+      if constexpr (KV == KV_SAME) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vw[j] = cur.v[i][j];
+      } else {
+        deq_pairs(cur.v[i], cur.vsc[i], vw);
+      }
+#pragma unroll
+      for (int j = 0; j < QW; ++j) {
+        vf[2 * j] = Pair<QT>::lo(vw[j]);
+        vf[2 * j + 1] = Pair<QT>::hi(vw[j]);
+      }
+#pragma unroll
+      for (int g = 0; g < HG; ++g) {
+        const float pg = pv[g * NI + i];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(pg, vf[e], acc[g][e]);
+      }
+    }
+  }
+
+  // ---- merge rows of the wave (same m), then the waves of the workgroup ----
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) {
+    float l = within_quad<OpAdd, LPH>(l_run[hh]);
+    l_run[hh] = across_rows<OpAdd, LPR>(l);
+  }
+#pragma unroll
+  for (int g = 0; g < HG; ++g)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = across_rows<OpAdd, LPR>(acc[g][e]);
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < HG; ++g)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s_red[w][g][c * EPL + e] = acc[g][e];
+#pragma unroll
+    for (int hh = 0; hh < HPL; ++hh) {
+      const int j0 = c * NPL + hh * VPH;
+      if (j0 % NI == 0) {
+        s_ml[w][j0 / NI][0] = m_run[hh];
+        s_ml[w][j0 / NI][1] = l_run[hh];
+      }
+    }
+  }
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < HG * D; idx += NW * 64) {
+    const int g = idx / D;
+    const int d = idx % D;
+    if (g >= nvalid) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_ml[ww][g][0]);
+    float A = 0.f, L = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        const float f = fast_exp2(s_ml[ww][g][0] - M);
+        A = __builtin_fmaf(s_red[ww][g][d], f, A);
+        L = __builtin_fmaf(s_ml[ww][g][1], f, L);
+      }
+    }
+    const int h = head0 + g;
+    if (S == 1) {
+      const float o = L > 0.f ? A / L : 0.f;
+      uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + (b * p.o_sb + h * p.o_sh + d);
+      *op = Pair<QT>::from_float(o);
+    } else {
+      const int64_t row = ((int64_t)b * p.H + h) * S + split;
+      p.ws_acc[row * D + d] = A;
+      if (d == 0) {
+        p.ws_ml[row * 2 + 0] = M;
+        p.ws_ml[row * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
+//   M = max_s m_s, w_s = 2^(m_s - M), o = sum_s acc_s w_s / sum_s l_s w_s.
+template <typename QT>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ ws_acc,
+                                                           const float* __restrict__ ws_ml, uint8_t* out,
+                                                           int B, int H, int D, int S, int64_t o_sb,
+                                                           int64_t o_sh) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)B * H * D) return;
+  const int d = idx % D;
+  const int64_t bh = idx / D;
+  const int h = bh % H;
+  const int b = bh / H;
+  const float* ml = ws_ml + bh * S * 2;
+  const float* acc = ws_acc + bh * S * D + d;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+  float A = 0.f, L = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < S; ++s) {
+      const float f = fast_exp2(ml[2 * s] - M);
+      A = __builtin_fmaf(acc[(int64_t)s * D], f, A);
+      L = __builtin_fmaf(ml[2 * s + 1], f, L);
+    }
+  }
+  const float o = L > 0.f ? A / L : 0.f;
+  uint16_t* op = reinterpret_cast<uint16_t*>(out) + (b * o_sb + h * o_sh + d);
+  *op = Pair<QT>::from_float(o);
+}
+
+}  // namespace fat
+
+// ===========================================================================
+// Host side
+// ===========================================================================
+namespace {
+
+int ilog2_exact(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int l = 0;
+  while ((1 << l) < x) ++l;
+  return l;
+}
+
+template <typename QT, int KV, int D, int HG>
+int launch_decode_t(const fat::DecodeParams& prm, int nw, dim3 grid, hipStream_t stream) {
+  if (nw == 8) {
+    hipLaunchKernelGGL((fat::paged_decode_kernel<QT, KV, D, HG, 8>), grid, dim3(8 * 64), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((fat::paged_decode_kernel<QT, KV, D, HG, 4>), grid, dim3(4 * 64), 0, stream, prm);
+  }
+  return fat_host::launch_status("paged_decode_kernel");
+}
+
+template <typename QT, int KV>
+int launch_decode_kv(const fat::DecodeParams& prm, int D, int HG, int nw, dim3 grid, hipStream_t stream) {
+  if (D == 128) {
+    return HG == 8 ? launch_decode_t<QT, KV, 128, 8>(prm, nw, grid, stream)
+                   : launch_decode_t<QT, KV, 128, 4>(prm, nw, grid, stream);
+  }
+  return HG == 8 ? launch_decode_t<QT, KV, 64, 8>(prm, nw, grid, stream)
+                 : launch_decode_t<QT, KV, 64, 4>(prm, nw, grid, stream);
+}
+
+template <typename QT>
+int launch_decode_q(const fat::DecodeParams& prm, int kv, int D, int HG, int nw, dim3 grid,
+                    hipStream_t stream) {
+  switch (kv) {
+    case fat::KV_SAME: return launch_decode_kv<QT, fat::KV_SAME>(prm, D, HG, nw, grid, stream);
+    case fat::KV_I8: return launch_decode_kv<QT, fat::KV_I8>(prm, D, HG, nw, grid, stream);
+    default: return launch_decode_kv<QT, fat::KV_FP8>(prm, D, HG, nw, grid, stream);
+  }
+}
+
+}  // namespace
+
+extern "C" size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                                   int32_t split_k) {
+  if (split_k <= 1 || batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return (size_t)batch * num_heads * split_k * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
+  fat_host::clear_error();
+  if (!a) {
+    fat_host::set_error("fat_paged_decode: args is NULL");
+    return FAT_E_INVALID;
+  }
+  if (!a->q || !a->k_cache || !a->v_cache || !a->page_table || !a->seq_lens || !a->out) {
+    fat_host::set_error("fat_paged_decode: a required pointer is NULL");
+    return FAT_E_INVALID;
+  }
+  if (a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->num_pages <= 0 || a->max_pages <= 0) {
+    fat_host::set_error("fat_paged_decode: batch, heads, num_pages and max_pages must be positive");
+    return FAT_E_INVALID;
+  }
+  if (a->num_heads % a->num_kv_heads != 0) {
+    fat_host::set_error("fat_paged_decode: num_heads %d must be divisible by num_kv_heads %d", a->num_heads,
+                        a->num_kv_heads);
+    return FAT_E_INVALID;
+  }
+  if (a->split_k < 1 || a->split_k > 64) {
+    fat_host::set_error("fat_paged_decode: split_k must be in [1, 64], got %d", a->split_k);
+    return FAT_E_INVALID;
+  }
+  if (a->q_dtype != FAT_DTYPE_F16 && a->q_dtype != FAT_DTYPE_BF16) {
+    fat_host::set_error("fat_paged_decode: q_dtype must be fp16 or bf16");
+    return FAT_E_UNSUPPORTED;
+  }
+  int kv;
+  if (a->kv_dtype == a->q_dtype) kv = fat::KV_SAME;
+  else if (a->kv_dtype == FAT_DTYPE_I8) kv = fat::KV_I8;
+  else if (a->kv_dtype == FAT_DTYPE_FP8E4M3) kv = fat::KV_FP8;
+  else {
+    fat_host::set_error("fat_paged_decode: kv_dtype must equal q_dtype or be int8/fp8e4m3");
+    return FAT_E_UNSUPPORTED;
+  }
+  if (kv != fat::KV_SAME && (!a->k_scale || !a->v_scale)) {
+    fat_host::set_error("fat_paged_decode: int8/fp8 K/V need k_scale and v_scale");
+    return FAT_E_INVALID;
+  }
+  const int D = a->head_dim;
+  if (D != 64 && D != 128) {
+    fat_host::set_error("fat_paged_decode: head_dim %d unsupported (64 or 128)", D);
+    return FAT_E_UNSUPPORTED;
+  }
+  const int log2P = ilog2_exact(a->page_size);
+  const int rpl = (kv == fat::KV_SAME) ? (D == 128 ? 4 : 8) : (D == 128 ? 8 : 16);
+  if (log2P < 0 || a->page_size < rpl) {
+    fat_host::set_error("fat_paged_decode: page_size %d unsupported (power of two >= %d for this head_dim/dtype)",
+                        a->page_size, rpl);
+    return FAT_E_UNSUPPORTED;
+  }
+  if (a->waves_per_group != 0 && a->waves_per_group != 4 && a->waves_per_group != 8) {
+    fat_host::set_error("fat_paged_decode: waves_per_group must be 0 (auto), 4 or 8, got %d", a->waves_per_group);
+    return FAT_E_INVALID;
+  }
+  if (a->split_k > 1 && !a->workspace) {
+    fat_host::set_error("fat_paged_decode: split_k > 1 needs a workspace");
+    return FAT_E_INVALID;
+  }
+  // 16-byte alignment of every row start the kernel loads.
+  const int eb = (kv == fat::KV_SAME) ? 2 : 1;
+  const uintptr_t align_or = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
+                             (uintptr_t)(2 * a->q_stride_b) | (uintptr_t)(2 * a->q_stride_h) |
+                             (uintptr_t)(eb * a->k_stride_page) | (uintptr_t)(eb * a->k_stride_slot) |
+                             (uintptr_t)(eb * a->k_stride_head) | (uintptr_t)(eb * a->v_stride_page) |
+                             (uintptr_t)(eb * a->v_stride_slot) | (uintptr_t)(eb * a->v_stride_head);
+  if (align_or & 15) {
+    fat_host::set_error("fat_paged_decode: q/K/V base pointers and row strides must be 16-byte aligned");
+    return FAT_E_INVALID;
+  }
+
+  const int group = a->num_heads / a->num_kv_heads;
+  const int HG = group >= 8 ? 8 : 4;
+  const int hg_per_kv = (group + HG - 1) / HG;
+
+  fat::DecodeParams prm{};
+  prm.q = static_cast<const uint8_t*>(a->q);
+  prm.k = static_cast<const uint8_t*>(a->k_cache);
+  prm.v = static_cast<const uint8_t*>(a->v_cache);
+  prm.ks = a->k_scale;
+  prm.vs = a->v_scale;
+  prm.pt = a->page_table;
+  prm.lens = a->seq_lens;
+  prm.out = static_cast<uint8_t*>(a->out);
+  const size_t acc_elems = (size_t)a->batch * a->num_heads * a->split_k * D;
+  prm.ws_acc = a->split_k > 1 ? static_cast<float*>(a->workspace) : nullptr;
+  prm.ws_ml = a->split_k > 1 ? static_cast<float*>(a->workspace) + acc_elems : nullptr;
+  prm.q_sb = a->q_stride_b;
+  prm.q_sh = a->q_stride_h;
+  prm.k_sp = a->k_stride_page;
+  prm.k_ss = a->k_stride_slot;
+  prm.k_sh = a->k_stride_head;
+  prm.v_sp = a->v_stride_page;
+  prm.v_ss = a->v_stride_slot;
+  prm.v_sh = a->v_stride_head;
+  prm.sc_sp = a->scale_stride_page;
+  prm.sc_sh = a->scale_stride_head;
+  prm.pt_sb = a->page_table_stride;
+  prm.o_sb = a->out_stride_b;
+  prm.o_sh = a->out_stride_h;
+  prm.H = a->num_heads;
+  prm.Hkv = a->num_kv_heads;
+  prm.group = group;
+  prm.hg_per_kv = hg_per_kv;
+  prm.P = a->page_size;
+  prm.log2P = log2P;
+  prm.num_pages = a->num_pages;
+  prm.max_pages = a->max_pages;
+  prm.scale_log2 = a->softmax_scale * fat::kLog2e;
+
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const dim3 grid(a->split_k, a->num_kv_heads * hg_per_kv, a->batch);
+  // Fewer than two 4-wave workgroups per CU leave the MI355X's 256 CUs short
+  // of loads in flight; use 8-wave workgroups then.
+  const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
+  const int nw = a->waves_per_group ? a->waves_per_group : (wgs < 2 * 256 ? 8 : 4);
+  int rc = (a->q_dtype == FAT_DTYPE_F16) ? launch_decode_q<fat::F16>(prm, kv, D, HG, nw, grid, stream)
+                                         : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);
+  if (rc != FAT_OK || a->split_k == 1) return rc;
+
+  const int64_t n = (int64_t)a->batch * a->num_heads * D;
+  const dim3 mgrid((unsigned)((n + 255) / 256));
+  if (a->q_dtype == FAT_DTYPE_F16) {
+    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::F16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
+                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+  } else {
+    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::BF16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
+                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+  }
+  return fat_host::launch_status("decode_merge_kernel");
+}

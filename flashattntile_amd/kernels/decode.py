@@ -1,0 +1,210 @@
+"""Paged decode on MI355X: host side of the HIP kernels in ``csrc/decode.hip``.
+
+Public functions keep the reference signatures and validation
+(``flashattn_tile/kernels/decode.py:474-704``):
+
+* :func:`paged_decode_attention` (fp16/bf16 cache, ``decode.py:533``);
+* :func:`paged_decode_attention_fp8` (int8 / float8_e4m3fn cache with
+  per-(page, KV-head) scales, ``decode.py:645``).
+
+Differences, all deliberate:
+
+* there is no CPU or Triton fallback: non-ROCm tensors, or a dtype the HIP
+  kernels do not take, raise instead of silently running the fp32 reference
+  (the oracle lives outside the product, under ``oracle/``);
+* the quantised path supports split-K as well;
+* ``config=None`` picks split-K from the MI355X occupancy heuristic
+  (:func:`flashattntile_amd.autotune.decode_split_k`) instead of an L4-tuned
+  JSON store; an explicit ``split_k`` is honoured exactly;
+* validation costs one device->host synchronisation instead of ~6.
+
+:func:`paged_decode_launch` is the sync-free entry below the validation, for
+callers (benchmarks, CUDA-graph-style capture loops) that validated once.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+from ..autotune import decode_split_k
+from ..paging import PagedKVCache, _check_layout, cache_stats
+
+__all__ = [
+    "DEFAULT_CONFIG",
+    "paged_decode_attention",
+    "paged_decode_attention_fp8",
+    "paged_decode_launch",
+]
+
+# split_k None -> MI355X heuristic; num_warps is the number of 64-lane waves
+# per workgroup (4 or 8; None lets the library choose from the grid size);
+# num_stages is accepted for signature compatibility with the reference's
+# Triton knob and validated the same way, but the HIP kernel's pipeline depth
+# is fixed (one 16-token unit prefetched per wave).
+DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2}
+
+_QUANT_DTYPES = tuple(d for d in (torch.int8, getattr(torch, "float8_e4m3fn", None)) if d is not None)
+
+
+def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache) -> dict:
+    resolved = dict(DEFAULT_CONFIG)
+    if config is not None:
+        unknown = set(config) - set(DEFAULT_CONFIG)
+        if unknown:
+            raise ValueError(f"unknown decode config keys: {sorted(unknown)}")
+        resolved.update(config)
+    if resolved["split_k"] is None:
+        resolved["split_k"] = decode_split_k(int(q.shape[0]), int(q.shape[1]), cache.num_kv_heads,
+                                             cache.max_pages_per_seq)
+    split_k = resolved["split_k"]
+    if not isinstance(split_k, int) or isinstance(split_k, bool) or split_k < 1:
+        raise ValueError(f"split_k must be a positive integer, got {split_k}")
+    if split_k > 64:
+        raise ValueError(f"split_k must be <= 64, got {split_k}")
+    if resolved["num_warps"] not in (None, 1, 2, 4, 8, 16, 32):
+        raise ValueError(f"num_warps must be a power of two <= 32, got {resolved['num_warps']}")
+    if resolved["num_warps"] not in (None, 4, 8):
+        raise ValueError(f"num_warps must be 4 or 8 waves per workgroup on MI355X, got {resolved['num_warps']}")
+    if resolved["num_stages"] < 1:
+        raise ValueError(f"num_stages must be >= 1, got {resolved['num_stages']}")
+    return resolved
+
+
+def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
+    """``decode.py:503-522`` + ``paging.validate_cache``, with one sync."""
+    if not isinstance(cache, PagedKVCache):
+        raise TypeError("cache must be a PagedKVCache")
+    _check_layout(cache)
+    if q.dim() != 3:
+        raise ValueError(f"q must be [batch, heads, head_dim], got {tuple(q.shape)}")
+    if q.shape[0] != cache.batch_size:
+        raise ValueError(f"q batch {q.shape[0]} != cache batch {cache.batch_size}")
+    if q.shape[2] != cache.head_dim:
+        raise ValueError(f"q head_dim {q.shape[2]} != cache head_dim {cache.head_dim}")
+    if q.shape[1] % cache.num_kv_heads != 0:
+        raise ValueError(f"num_heads {q.shape[1]} must be divisible by num_kv_heads {cache.num_kv_heads}")
+    if q.device != cache.k_cache.device:
+        raise ValueError("q and cache must live on the same device")
+    if not q.is_floating_point():
+        raise ValueError(f"q must be floating point, got {q.dtype}")
+    min_len, max_len, lo, hi = cache_stats(cache)
+    if min_len < 0:
+        raise AssertionError("seq_lens must be non-negative")
+    capacity = cache.capacity
+    if max_len > capacity:
+        raise AssertionError(f"seq_len {max_len} exceeds page-table capacity {capacity}")
+    if max_len > 0:
+        if lo < 0:
+            raise AssertionError("page_table contains a negative page id")
+        if hi >= cache.num_pages:
+            raise AssertionError(f"page_table references page {hi} but cache has {cache.num_pages} pages")
+    if min_len <= 0:
+        raise ValueError("decode requires every sequence to hold at least one cached token")
+
+
+def _require_rocm(q: torch.Tensor, cache: PagedKVCache, what: str) -> None:
+    tensors = (q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens)
+    if not all(t.is_cuda for t in tensors):
+        raise RuntimeError(
+            f"{what}: inputs must be ROCm device tensors; this build runs the gfx950 HIP kernel only "
+            "(no CPU or reference fallback)"
+        )
+
+
+def paged_decode_launch(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    softmax_scale: float,
+    split_k: int,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    scales=None,
+    waves_per_group: int | None = None,
+) -> torch.Tensor:
+    """Enqueue the HIP decode without validation or synchronisation.
+
+    ``q`` must be contiguous fp16/bf16 on the cache's device; ``out`` (default
+    ``empty_like(q)``) and ``workspace`` (default: allocated) may be passed in
+    to avoid allocations.
+    """
+    if cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
+        raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
+    if out is None:
+        out = torch.empty_like(q)
+    need = _hip.decode_workspace_bytes(q.shape[0], q.shape[1], q.shape[2], split_k)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    k_scale = v_scale = None
+    if scales is not None:
+        k_scale = scales["k"] if isinstance(scales, dict) else scales.k
+        v_scale = scales["v"] if isinstance(scales, dict) else scales.v
+    _hip.paged_decode(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, out,
+                      cache.page_size, softmax_scale, split_k, workspace=workspace,
+                      k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0)
+    return out
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    softmax_scale: float | None = None,
+    config: dict | None = None,
+    grouped: bool = False,
+) -> torch.Tensor:
+    """Paged decode attention, one query per sequence (``decode.py:533-642``).
+
+    ``q``: ``[batch, num_heads, head_dim]`` fp16/bf16 on a ROCm device; the
+    cache holds the same dtype.  ``softmax_scale`` defaults to
+    ``head_dim ** -0.5``.  ``config``: ``split_k`` (1 = no split; default from
+    the MI355X heuristic), ``num_warps``, ``num_stages``.  ``grouped`` is
+    accepted for compatibility: the HIP kernel always reads each K/V page
+    once per GQA group.  Returns ``[batch, num_heads, head_dim]`` in
+    ``q.dtype``.
+    """
+    del grouped  # every launch is grouped on MI355X
+    _validate_decode_inputs(q, cache)
+    scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+    cfg = _resolve_config(config, q, cache)
+    _require_rocm(q, cache, "paged_decode_attention")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"paged_decode_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    if cache.k_cache.dtype != q.dtype:
+        raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
+    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"])
+
+
+def paged_decode_attention_fp8(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    scales,
+    softmax_scale: float | None = None,
+    config: dict | None = None,
+) -> torch.Tensor:
+    """Decode against an int8 / float8_e4m3fn cache (``decode.py:645-704``).
+
+    ``scales`` is a :class:`~flashattntile_amd.quant.QuantScales` (or a dict
+    with ``"k"``/``"v"``), fp32 ``[num_pages, num_kv_heads]``.  Pages are
+    dequantised in registers as ``(float(x) * scale).to(q.dtype)``.
+    """
+    _validate_decode_inputs(q, cache)
+    k_scale = scales["k"] if isinstance(scales, dict) else scales.k
+    v_scale = scales["v"] if isinstance(scales, dict) else scales.v
+    quant_dtype = cache.k_cache.dtype
+    if quant_dtype not in _QUANT_DTYPES:
+        raise ValueError(f"expected int8/float8 cache, got {quant_dtype}")
+    expected = (cache.num_pages, cache.num_kv_heads)
+    if tuple(k_scale.shape) != expected or tuple(v_scale.shape) != expected:
+        raise ValueError(f"scales must have shape {expected}, got {tuple(k_scale.shape)}")
+    scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+    cfg = _resolve_config(config, q, cache)
+    _require_rocm(q, cache, "paged_decode_attention_fp8")
+    if not (k_scale.is_cuda and v_scale.is_cuda):
+        raise RuntimeError("paged_decode_attention_fp8: scales must be ROCm device tensors")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"quantised decode requires fp16/bf16 queries, got {q.dtype}")
+    if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
+        raise ValueError("scales must be float32")
+    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"],
+                               scales={"k": k_scale.contiguous(), "v": v_scale.contiguous()},
+                               waves_per_group=cfg["num_warps"])

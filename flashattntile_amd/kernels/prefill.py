@@ -1,0 +1,165 @@
+"""Varlen (packed) prefill attention on MI355X: host side of ``csrc/prefill.hip``.
+
+Keeps the reference signature, config keys and validation
+(``flashattn_tile/kernels/prefill.py:145-326``).  The HIP kernel runs QK^T
+and PV on CDNA4 MFMA (v_mfma_f32_32x32x16_{f16,bf16}) with fp32
+accumulation; the Triton tile knobs (BLOCK_M/BLOCK_N/num_warps/num_stages)
+are validated as in the reference but the gfx950 kernel uses its own fixed
+tiling.  There is no CPU fallback: non-ROCm tensors or a dtype other than
+fp16/bf16 raise.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+
+__all__ = ["DEFAULT_CONFIG", "prefill_attention", "prefill_launch"]
+
+DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3}
+
+
+def _resolve_config(config: dict | None) -> dict:
+    resolved = dict(DEFAULT_CONFIG)
+    if config is not None:
+        unknown = set(config) - set(DEFAULT_CONFIG)
+        if unknown:
+            raise ValueError(f"unknown prefill config keys: {sorted(unknown)}")
+        resolved.update(config)
+    for key in ("BLOCK_M", "BLOCK_N"):
+        val = resolved[key]
+        if val <= 0 or val & (val - 1):
+            raise ValueError(f"{key} must be a positive power of two, got {val}")
+    if resolved["num_warps"] not in (1, 2, 4, 8, 16, 32):
+        raise ValueError(f"num_warps must be a power of two <= 32, got {resolved['num_warps']}")
+    if resolved["num_stages"] < 1:
+        raise ValueError(f"num_stages must be >= 1, got {resolved['num_stages']}")
+    return resolved
+
+
+def _validate_inputs(q, k, v, cu_seqlens_q, cu_seqlens_k, causal) -> tuple[int, int]:
+    """``prefill.py:194-233`` with the device-side checks in one sync.
+
+    Returns the longest query and key sequence lengths."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k, v must be 3-D [tokens, heads, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"k shape {tuple(k.shape)} != v shape {tuple(v.shape)}")
+    if q.shape[-1] != k.shape[-1]:
+        raise ValueError(f"q head_dim {q.shape[-1]} != k head_dim {k.shape[-1]}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError(f"dtype mismatch: q {q.dtype}, k {k.dtype}, v {v.dtype}")
+    if not q.is_floating_point():
+        raise ValueError(f"expected floating point inputs, got {q.dtype}")
+    if q.device != k.device or k.device != v.device:
+        raise ValueError("q, k, v must live on the same device")
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_k.dim() != 1:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must be 1-D")
+    if cu_seqlens_q.shape[0] != cu_seqlens_k.shape[0]:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must have the same batch dimension")
+    if cu_seqlens_q.numel() < 2:
+        raise ValueError("cu_seqlens must contain at least batch + 1 entries")
+    if cu_seqlens_q.dtype != torch.int32 or cu_seqlens_k.dtype != torch.int32:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must be int32")
+    if cu_seqlens_q.device != q.device or cu_seqlens_k.device != q.device:
+        raise ValueError("cu_seqlens must live on the same device as q")
+    cq = cu_seqlens_q.to(torch.int64)
+    ck = cu_seqlens_k.to(torch.int64)
+    lq = cq[1:] - cq[:-1]
+    lk = ck[1:] - ck[:-1]
+    stats = torch.stack([
+        cq[0], ck[0], cq[-1], ck[-1],
+        (lq < 0).any().to(torch.int64), (lk < 0).any().to(torch.int64),
+        (lk < lq).any().to(torch.int64), lq.max(), lk.max(),
+    ]).cpu().tolist()
+    q0, k0, q_end, k_end, q_dec, k_dec, short_kv, max_q, max_k = (int(x) for x in stats)
+    if q0 != 0 or k0 != 0:
+        raise ValueError("cu_seqlens must start at 0")
+    if q_end != q.shape[0]:
+        raise ValueError("cu_seqlens_q[-1] must equal q.shape[0]")
+    if k_end != k.shape[0]:
+        raise ValueError("cu_seqlens_k[-1] must equal k.shape[0]")
+    if q_dec:
+        raise ValueError("cu_seqlens_q must be non-decreasing")
+    if k_dec:
+        raise ValueError("cu_seqlens_k must be non-decreasing")
+    if causal and short_kv:
+        raise ValueError("causal bottom-right alignment requires kv_len >= q_len per sequence")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError(f"num_heads ({q.shape[1]}) must be divisible by num_kv_heads ({k.shape[1]})")
+    return max_q, max_k
+
+
+def prefill_launch(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    causal: bool,
+    softmax_scale: float,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Enqueue the HIP prefill without validation or synchronisation.
+
+    ``q``/``k``/``v`` must have a contiguous head_dim axis; ``max_seqlen_*``
+    must bound every sequence (they size the launch grid).
+    """
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("q, k, v need a contiguous head_dim axis")
+    if out is None:
+        out = torch.empty_like(q)
+    need = _hip.prefill_workspace_bytes(k.shape[0], k.shape[1], k.shape[2])
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _hip.prefill_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k,
+                        causal, softmax_scale, workspace=workspace)
+    return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    causal: bool = True,
+    softmax_scale: float | None = None,
+    config: dict | None = None,
+) -> torch.Tensor:
+    """Fused varlen prefill attention (``prefill.py:236-326``).
+
+    ``q``: ``[total_q, num_heads, head_dim]``; ``k``/``v``:
+    ``[total_k, num_kv_heads, head_dim]``; ``cu_seqlens_*`` int32 ``[B + 1]``
+    on the same ROCm device; causal masking is bottom-right aligned.  Returns
+    ``[total_q, num_heads, head_dim]`` in ``q.dtype``.
+    """
+    longest_q, longest_k = _validate_inputs(q, k, v, cu_seqlens_q, cu_seqlens_k, causal)
+    scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+    if max_seqlen_q <= 0:
+        raise ValueError(f"max_seqlen_q must be positive, got {max_seqlen_q}")
+    if max_seqlen_k <= 0:
+        raise ValueError(f"max_seqlen_k must be positive, got {max_seqlen_k}")
+    # The grid is sized from max_seqlen_q; a smaller bound would leave rows
+    # uncomputed, so it is checked against cu_seqlens (no extra sync).
+    if max_seqlen_q < longest_q:
+        raise ValueError(f"max_seqlen_q {max_seqlen_q} is smaller than the longest query sequence {longest_q}")
+    if max_seqlen_k < longest_k:
+        raise ValueError(f"max_seqlen_k {max_seqlen_k} is smaller than the longest key sequence {longest_k}")
+    _resolve_config(config)
+    if not all(t.is_cuda for t in (q, k, v, cu_seqlens_q, cu_seqlens_k)):
+        raise RuntimeError("prefill_attention: inputs must be ROCm device tensors; this build runs the gfx950 "
+                           "HIP kernel only (no CPU or reference fallback)")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    return prefill_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
+                          bool(causal), scale)

@@ -1,0 +1,257 @@
+"""Paged KV-cache contract: NHD pages, an int32 block table and int32 lengths.
+
+Drop-in for ``flashattn_tile/paging.py`` (same names, fields, error types and
+messages; reference lines cited per function).  The kernels read exactly this
+layout:
+
+``k_cache`` / ``v_cache``
+    ``[num_pages, page_size, num_kv_heads, head_dim]``; head_dim contiguous.
+    A quantised cache stores ``int8`` or ``float8_e4m3fn`` elements.
+``page_table``
+    ``int32 [batch, max_pages_per_seq]``: ``page_table[b, i]`` is the physical
+    page holding logical block ``i`` of sequence ``b``; entries past
+    ``ceil(seq_lens[b] / page_size)`` are never read.
+``seq_lens``
+    ``int32 [batch]`` valid tokens; token ``t`` of sequence ``b`` lives in page
+    ``page_table[b, t // page_size]`` at slot ``t % page_size``.
+
+On MI355X the whole pool is one allocation in HBM (288 GB per GPU holds e.g.
+a 32-sequence x 4096-token fp16 cache of 32 KiB pages in 512 MiB); pages are
+addressed through the table so a serving engine may permute them freely.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+__all__ = [
+    "PagedKVCache",
+    "validate_cache",
+    "allocate",
+    "append_tokens",
+    "gather_paged",
+    "gather_contiguous",
+]
+
+
+@dataclass
+class PagedKVCache:
+    """Paged K/V cache plus its page table (``paging.py:30-76``)."""
+
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    page_table: torch.Tensor
+    seq_lens: torch.Tensor
+    page_size: int
+
+    @property
+    def batch_size(self) -> int:
+        return int(self.seq_lens.shape[0])
+
+    @property
+    def num_pages(self) -> int:
+        return int(self.k_cache.shape[0])
+
+    @property
+    def num_kv_heads(self) -> int:
+        return int(self.k_cache.shape[2])
+
+    @property
+    def head_dim(self) -> int:
+        return int(self.k_cache.shape[3])
+
+    @property
+    def max_pages_per_seq(self) -> int:
+        return int(self.page_table.shape[1])
+
+    @property
+    def capacity(self) -> int:
+        """Maximum tokens per sequence addressable by the page table."""
+        return self.max_pages_per_seq * self.page_size
+
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise AssertionError(message)
+
+
+def _check_layout(cache: PagedKVCache) -> None:
+    """Host-only shape/dtype/device checks (no device synchronisation)."""
+    _require(isinstance(cache, PagedKVCache), "cache must be a PagedKVCache")
+    k, v = cache.k_cache, cache.v_cache
+    _require(k.dim() == 4, f"k_cache must be 4-D [pages, page_size, kv_heads, dim], got {tuple(k.shape)}")
+    _require(k.shape == v.shape, f"k_cache {tuple(k.shape)} and v_cache {tuple(v.shape)} must match")
+    _require(k.dtype == v.dtype, f"k_cache dtype {k.dtype} != v_cache dtype {v.dtype}")
+    _require(k.device == v.device, "k_cache and v_cache must live on the same device")
+    _require(cache.page_size > 0, "page_size must be positive")
+    _require(k.shape[1] == cache.page_size, f"k_cache page dim {k.shape[1]} != page_size {cache.page_size}")
+    pt, sl = cache.page_table, cache.seq_lens
+    _require(pt.dtype == torch.int32, f"page_table must be int32, got {pt.dtype}")
+    _require(sl.dtype == torch.int32, f"seq_lens must be int32, got {sl.dtype}")
+    _require(pt.dim() == 2, "page_table must be [batch, max_pages_per_seq]")
+    _require(sl.dim() == 1, "seq_lens must be [batch]")
+    _require(pt.shape[0] == sl.shape[0], "page_table and seq_lens batch dimensions disagree")
+    _require(pt.device == sl.device, "page_table and seq_lens must live on the same device")
+
+
+def cache_stats(cache: PagedKVCache) -> tuple[int, int, int, int]:
+    """``(min_len, max_len, min_page, max_page)`` in ONE device->host copy.
+
+    The page range covers ``page_table[:, :ceil(max_len / page_size)]`` for every
+    row, the same entries ``paging.py:123-129`` inspects.  With no cached token
+    the page range is reported as ``(0, -1)``.
+    """
+    sl = cache.seq_lens
+    pt = cache.page_table
+    if sl.numel() == 0:
+        return 0, 0, 0, -1
+    max_len = sl.max()
+    need = torch.div(max_len + (cache.page_size - 1), cache.page_size, rounding_mode="floor")
+    cols = torch.arange(pt.shape[1], device=pt.device)
+    used = (cols < need).unsqueeze(0).expand_as(pt)
+    big = torch.iinfo(torch.int32).max
+    small = torch.iinfo(torch.int32).min
+    if pt.numel():
+        min_page = torch.where(used, pt, torch.full_like(pt, big)).min()
+        max_page = torch.where(used, pt, torch.full_like(pt, small)).max()
+    else:
+        min_page = torch.tensor(big, dtype=torch.int32, device=pt.device)
+        max_page = torch.tensor(small, dtype=torch.int32, device=pt.device)
+    stats = torch.stack([sl.min().to(torch.int64), max_len.to(torch.int64),
+                         min_page.to(torch.int64), max_page.to(torch.int64)]).cpu().tolist()
+    min_len, max_len_i, lo, hi = (int(x) for x in stats)
+    if lo == big:
+        lo, hi = 0, -1
+    return min_len, max_len_i, lo, hi
+
+
+def validate_cache(cache: PagedKVCache, *, check_pages: bool = True) -> tuple[int, int]:
+    """Validate shapes, dtypes, page bounds and lengths (``paging.py:84-130``).
+
+    Raises ``AssertionError`` naming the offending field.  Returns
+    ``(min_len, max_len)`` so callers need no further synchronisation.
+    """
+    _check_layout(cache)
+    min_len, max_len, lo, hi = cache_stats(cache)
+    _require(min_len >= 0, "seq_lens must be non-negative")
+    capacity = cache.max_pages_per_seq * cache.page_size
+    _require(max_len <= capacity, f"seq_len {max_len} exceeds page-table capacity {capacity}")
+    if check_pages and max_len > 0:
+        _require(lo >= 0, "page_table contains a negative page id")
+        _require(hi < cache.num_pages, f"page_table references page {hi} but cache has {cache.num_pages} pages")
+    return min_len, max_len
+
+
+def allocate(
+    batch: int,
+    max_seq_len: int,
+    num_kv_heads: int,
+    head_dim: int,
+    page_size: int,
+    dtype: torch.dtype = torch.float16,
+    device: torch.device | str = "cpu",
+) -> PagedKVCache:
+    """Zeroed cache with the contiguous mapping ``page_table[b, i] = b * pages + i``
+    (``paging.py:133-169``)."""
+    _require(batch > 0, "batch must be positive")
+    _require(max_seq_len > 0, "max_seq_len must be positive")
+    _require(num_kv_heads > 0 and head_dim > 0, "num_kv_heads and head_dim must be positive")
+    _require(page_size > 0, "page_size must be positive")
+    allowed = {torch.float16, torch.bfloat16, torch.float32, torch.int8}
+    if getattr(torch, "float8_e4m3fn", None) is not None:
+        allowed.add(torch.float8_e4m3fn)
+    _require(dtype in allowed, f"unsupported cache dtype {dtype}")
+    pages_per_seq = math.ceil(max_seq_len / page_size)
+    num_pages = batch * pages_per_seq
+    shape = (num_pages, page_size, num_kv_heads, head_dim)
+    cache = PagedKVCache(
+        k_cache=torch.zeros(shape, dtype=dtype, device=device),
+        v_cache=torch.zeros(shape, dtype=dtype, device=device),
+        page_table=torch.arange(num_pages, dtype=torch.int32, device=device).view(batch, pages_per_seq),
+        seq_lens=torch.zeros(batch, dtype=torch.int32, device=device),
+        page_size=page_size,
+    )
+    validate_cache(cache)
+    return cache
+
+
+def append_tokens(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor) -> None:
+    """Write one token per sequence at position ``seq_lens[b]`` through the page
+    table, then increment ``seq_lens`` in place (``paging.py:172-210``)."""
+    validate_cache(cache, check_pages=False)
+    expect = (cache.batch_size, cache.num_kv_heads, cache.head_dim)
+    _require(new_k.shape == expect,
+             f"new_k must be [{expect[0]}, {expect[1]}, {expect[2]}], got {tuple(new_k.shape)}")
+    _require(new_v.shape == new_k.shape, f"new_v shape {tuple(new_v.shape)} != new_k shape {tuple(new_k.shape)}")
+    _require(new_k.dtype == cache.k_cache.dtype, f"new_k dtype {new_k.dtype} != cache dtype {cache.k_cache.dtype}")
+    _require(new_v.dtype == cache.k_cache.dtype, f"new_v dtype {new_v.dtype} != cache dtype {cache.k_cache.dtype}")
+    _require(new_k.device == cache.k_cache.device, "new_k must be on the cache device")
+    _require(new_v.device == cache.k_cache.device, "new_v must be on the cache device")
+
+    pos = cache.seq_lens.long()
+    block = torch.div(pos, cache.page_size, rounding_mode="floor")
+    rows = torch.arange(cache.batch_size, device=cache.page_table.device)
+    safe_block = block.clamp(max=cache.max_pages_per_seq - 1)
+    phys = cache.page_table[rows, safe_block].long()
+    # One synchronisation for all bounds checks.
+    max_pos, max_block, lo, hi = (int(x) for x in torch.stack(
+        [pos.max(), block.max(), phys.min(), phys.max()]).cpu().tolist())
+    _require(max_pos < cache.capacity, f"append would exceed page-table capacity {cache.capacity}")
+    _require(max_block < cache.max_pages_per_seq, "append would index past the page table")
+    _require(lo >= 0 and hi < cache.num_pages, f"page_table maps to a page outside [0, {cache.num_pages})")
+    slots = (pos % cache.page_size).to(cache.k_cache.device)
+    phys = phys.to(cache.k_cache.device)
+    cache.k_cache[phys, slots] = new_k
+    cache.v_cache[phys, slots] = new_v
+    cache.seq_lens += 1
+
+
+def gather_paged(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    page_size: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Padded contiguous copy ``[batch, max_len, kv_heads, dim]``; rows past a
+    sequence's length are zero (``paging.py:213-256``).  A debugging/reference
+    utility; the kernels never gather."""
+    _require(k_cache.shape == v_cache.shape, "k_cache and v_cache shapes must match")
+    _require(page_table.dtype == torch.int32, "page_table must be int32")
+    _require(seq_lens.dtype == torch.int32, "seq_lens must be int32")
+    _require(page_table.dim() == 2 and seq_lens.dim() == 1, "expected page_table [B, P] and seq_lens [B]")
+    _require(page_table.shape[0] == seq_lens.shape[0], "page_table / seq_lens batch mismatch")
+    _require(k_cache.shape[1] == page_size, "k_cache page dim != page_size")
+
+    batch = int(seq_lens.shape[0])
+    lens = [int(x) for x in seq_lens.cpu().tolist()]
+    max_len = max(lens) if batch else 0
+    hk, d = k_cache.shape[2], k_cache.shape[3]
+    out_k = k_cache.new_zeros((batch, max_len, hk, d))
+    out_v = v_cache.new_zeros((batch, max_len, hk, d))
+    if max_len == 0:
+        return out_k, out_v
+    capacity = int(page_table.shape[1]) * page_size
+    _require(max_len <= capacity, f"seq_len {max_len} exceeds page-table capacity {capacity}")
+
+    num_pages = int(k_cache.shape[0])
+    table = page_table.cpu()
+    for b, length in enumerate(lens):
+        if length == 0:
+            continue
+        ids = table[b, : math.ceil(length / page_size)].long()
+        _require(int(ids.min()) >= 0 and int(ids.max()) < num_pages,
+                 f"sequence {b} page id outside [0, {num_pages})")
+        ids = ids.to(k_cache.device)
+        out_k[b, :length] = k_cache.index_select(0, ids).reshape(-1, hk, d)[:length]
+        out_v[b, :length] = v_cache.index_select(0, ids).reshape(-1, hk, d)[:length]
+    return out_k, out_v
+
+
+def gather_contiguous(cache: PagedKVCache) -> tuple[torch.Tensor, torch.Tensor]:
+    """Validate, then gather ``cache`` into padded contiguous K/V."""
+    validate_cache(cache)
+    return gather_paged(cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, cache.page_size)

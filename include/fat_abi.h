@@ -1,0 +1,171 @@
+/*
+ * fat_abi.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * The shared library libfat_hip.so exports exactly the functions declared
+ * here.  Every entry point takes plain device pointers, element strides and
+ * sizes; no framework types cross this boundary.  The caller owns every
+ * buffer (inputs, outputs and the split-K workspace); the library never
+ * allocates, frees or synchronises, and enqueues its kernels on the
+ * hipStream_t passed as `stream` (NULL = the default stream).
+ *
+ * Return value: 0 on success, otherwise a FAT_E_* code; the matching message
+ * is available from fat_last_error() on the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the FlashAttnTile tree):
+ *   fat_paged_decode       flashattn_tile/kernels/decode.py:533-642
+ *                          (paged_decode_attention: _decode_paged_kernel,
+ *                          _decode_paged_split_kernel + _decode_reduce_kernel)
+ *                          and csrc/paged_decode.cu:297-344 (paged_decode_cuda,
+ *                          bound by csrc/bindings.cpp:14-20)
+ *   fat_paged_decode (int8/fp8 kv_dtype)
+ *                          flashattn_tile/kernels/decode.py:645-704
+ *                          (paged_decode_attention_fp8: _decode_paged_quant_kernel)
+ *   fat_prefill_varlen     flashattn_tile/kernels/prefill.py:236-326
+ *                          (prefill_attention: _fwd_varlen_kernel)
+ */
+#ifndef FAT_ABI_H
+#define FAT_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAT_ABI_VERSION 1
+
+/* Element types understood by the kernels. */
+enum fat_dtype {
+  FAT_DTYPE_F16 = 0,     /* IEEE binary16                                  */
+  FAT_DTYPE_BF16 = 1,    /* bfloat16                                       */
+  FAT_DTYPE_I8 = 2,      /* symmetric int8 KV storage (scale = absmax/127) */
+  FAT_DTYPE_FP8E4M3 = 3  /* OCP float8 e4m3fn KV storage (absmax/448)      */
+};
+
+/* Error codes. */
+enum fat_status {
+  FAT_OK = 0,
+  FAT_E_INVALID = 1,     /* bad argument (shape, dtype, pointer, stride)   */
+  FAT_E_UNSUPPORTED = 2, /* valid request this build has no kernel for     */
+  FAT_E_LAUNCH = 3       /* the HIP runtime rejected a launch              */
+};
+
+/*
+ * Paged decode: one query per sequence against a paged K/V cache.
+ *
+ * Layouts (NHD pages, flashattn_tile/paging.py:1-20):
+ *   q        [batch, num_heads, head_dim]          q_dtype
+ *   k_cache  [num_pages, page_size, num_kv_heads, head_dim]  kv_dtype
+ *   v_cache  same shape and dtype as k_cache
+ *   k_scale  [num_pages, num_kv_heads] fp32, only for int8/fp8 kv_dtype
+ *   v_scale  same as k_scale
+ *   page_table int32 [batch, max_pages]  (row stride page_table_stride)
+ *   seq_lens int32 [batch], every entry in [1, max_pages*page_size]
+ *   out      [batch, num_heads, head_dim]          q_dtype
+ * Strides are in elements; the head_dim axis must be contiguous.
+ *
+ * Query head h reads KV head h / (num_heads / num_kv_heads).  The context of
+ * sequence b is split into split_k partitions of ceil(ceil(len/P)/split_k)
+ * pages each; with split_k > 1 the partitions are merged by a log-sum-exp
+ * reduction through `workspace`, which must hold
+ * fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k) bytes
+ * (it may be NULL when split_k == 1).  int8/fp8 pages are dequantised as
+ * round_to_q_dtype(float(x) * scale) before the fp32 attention, exactly as
+ * dequantize_kv_pages (flashattn_tile/quant.py:145-161) followed by the fp32
+ * reference does.
+ */
+typedef struct fat_decode_args {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* page_table;
+  const int32_t* seq_lens;
+  void* out;
+  void* workspace;
+  int64_t q_stride_b, q_stride_h;
+  int64_t k_stride_page, k_stride_slot, k_stride_head;
+  int64_t v_stride_page, v_stride_slot, v_stride_head;
+  int64_t scale_stride_page, scale_stride_head;
+  int64_t page_table_stride;
+  int64_t out_stride_b, out_stride_h;
+  int32_t batch;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t num_pages;
+  int32_t max_pages;
+  int32_t split_k;
+  int32_t waves_per_group; /* 0 = chosen by the library, else 4 or 8 */
+  int32_t q_dtype;  /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 (also the out dtype) */
+  int32_t kv_dtype; /* q_dtype, FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3           */
+  float softmax_scale;
+} fat_decode_args;
+
+/*
+ * Packed varlen prefill (flash attention forward).
+ *   q   [total_q, num_heads, head_dim]      dtype
+ *   k,v [total_k, num_kv_heads, head_dim]   dtype
+ *   cu_seqlens_q / cu_seqlens_k int32 [batch + 1], starting at 0,
+ *   non-decreasing, kv_len >= q_len per sequence when causal.
+ *   out [total_q, num_heads, head_dim]      dtype
+ * Causal masking is bottom-right aligned: query i of a sequence sees key j
+ * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
+ * The kernel needs a workspace of fat_prefill_workspace_bytes(total_k,
+ * num_kv_heads, head_dim) bytes, used to stage V in key-major order.
+ */
+typedef struct fat_prefill_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* cu_seqlens_q;
+  const int32_t* cu_seqlens_k;
+  void* out;
+  void* workspace;
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_t, k_stride_h;
+  int64_t v_stride_t, v_stride_h;
+  int64_t out_stride_t, out_stride_h;
+  int32_t batch;
+  int32_t total_q;
+  int32_t total_k;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t max_seqlen_q;
+  int32_t max_seqlen_k;
+  int32_t causal;
+  int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
+  float softmax_scale;
+} fat_prefill_args;
+
+/* ABI version of the loaded library (FAT_ABI_VERSION at build time). */
+int fat_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fat_last_error(void);
+
+/* Bytes of split-K workspace fat_paged_decode needs (0 when split_k == 1). */
+size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads,
+                                        int32_t head_dim, int32_t split_k);
+
+/* Enqueue paged decode (fp16/bf16/int8/fp8 K/V) on `stream`.
+ * Replaces flashattn_tile/kernels/decode.py:533-704 (see file header). */
+int fat_paged_decode(const fat_decode_args* args, void* stream);
+
+/* Bytes of workspace fat_prefill_varlen needs. */
+size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
+                                   int32_t head_dim);
+
+/* Enqueue varlen prefill on `stream`.
+ * Replaces flashattn_tile/kernels/prefill.py:236-326 (see file header). */
+int fat_prefill_varlen(const fat_prefill_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAT_ABI_H */

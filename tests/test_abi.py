@@ -1,0 +1,119 @@
+"""The C-ABI library: loads, exports every symbol include/fat_abi.h declares,
+matches the ctypes struct layout, and rejects bad arguments before touching
+the device (no kernel runs here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from flashattntile_amd import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fat_abi.h"
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(fat_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    assert _hip.is_loaded(), _hip.load_error()
+    lib = _hip.lib()
+    declared = _declared_functions()
+    assert set(declared) == set(_hip.EXPORTED_SYMBOLS), declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(_hip.LIB_PATH)], capture_output=True, text=True).stdout
+        exported = set(re.findall(r"\bT (fat_\w+)", out))
+        assert exported == set(declared)
+
+
+def test_abi_version_and_workspace_sizes():
+    lib = _hip.lib()
+    assert lib.fat_abi_version() == _hip.ABI_VERSION
+    assert _hip.decode_workspace_bytes(32, 32, 128, 1) == 0
+    assert _hip.decode_workspace_bytes(32, 32, 128, 4) == 32 * 32 * 4 * 130 * 4
+    assert _hip.prefill_workspace_bytes(1, 1, 128) >= 0
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_ctypes(tmp_path):
+    src = tmp_path / "layout.c"
+    fields = {
+        "fat_decode_args": [f for f, _ in _hip.DecodeArgs._fields_],
+        "fat_prefill_args": [f for f, _ in _hip.PrefillArgs._fields_],
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for struct, names in fields.items():
+        lines.append(f'  printf("{struct} size %zu\\n", sizeof({struct}));')
+        for n in names:
+            lines.append(f'  printf("{struct} {n} %zu\\n", offsetof({struct}, {n}));')
+    lines.append("  return 0; }")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        struct, name, val = line.split()
+        got[(struct, name)] = int(val)
+    for struct, cls in (("fat_decode_args", _hip.DecodeArgs), ("fat_prefill_args", _hip.PrefillArgs)):
+        assert got[(struct, "size")] == ctypes.sizeof(cls)
+        for n, _ in cls._fields_:
+            assert got[(struct, n)] == getattr(cls, n).offset, (struct, n)
+
+
+def _err() -> str:
+    return _hip.lib().fat_last_error().decode()
+
+
+def test_decode_argument_errors_are_reported():
+    lib = _hip.lib()
+    assert lib.fat_paged_decode(None, None) == 1
+    assert "NULL" in _err()
+    a = _hip.DecodeArgs()
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1
+    assert "pointer is NULL" in _err()
+    # Non-null fake pointers: every rejection below happens before any launch.
+    for f in ("q", "k_cache", "v_cache", "page_table", "seq_lens", "out"):
+        setattr(a, f, 0x1000)
+    a.batch, a.num_heads, a.num_kv_heads, a.head_dim = 1, 4, 3, 128
+    a.page_size, a.num_pages, a.max_pages, a.split_k = 16, 1, 1, 1
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "divisible" in _err()
+    a.num_kv_heads = 2
+    a.split_k = 65
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "split_k" in _err()
+    a.split_k = 2
+    a.q_dtype = a.kv_dtype = _hip.DT_F16
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "workspace" in _err()
+    a.split_k = 1
+    a.head_dim = 96
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "head_dim" in _err()
+    a.head_dim = 128
+    a.page_size = 12
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "page_size" in _err()
+    a.page_size = 16
+    a.kv_dtype = _hip.DT_I8
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "scale" in _err()
+    a.kv_dtype = _hip.DT_F16
+    a.q_dtype = 9
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "q_dtype" in _err()
+    a.q_dtype = _hip.DT_F16
+    a.k_stride_slot = 3  # 6-byte rows: misaligned for 16-byte loads
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "aligned" in _err()
+
+
+def test_prefill_argument_errors_are_reported():
+    lib = _hip.lib()
+    assert lib.fat_prefill_varlen(None, None) == 1
+    a = _hip.PrefillArgs()
+    assert lib.fat_prefill_varlen(ctypes.byref(a), None) != 0
+    assert _err()

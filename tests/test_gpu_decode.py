@@ -1,0 +1,190 @@
+"""GPU parity of the HIP paged decode against the fp32 oracle.
+
+Inputs are unscaled N(0,1) (harsher than the reference tests' 0.2 factor),
+pages are scattered by a seeded permutation and the slots past each
+sequence's end are poisoned (K = 30, V = 500) so any masking error shows.
+Tolerance: 2e-3 on the kernel's result before its final rounding (see
+tests/_parity.py); quantised caches are compared with the oracle run on the
+cache dequantised to q.dtype (the reference's own dequantise-then-attend).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from _parity import assert_parity, make_paged, make_query
+from flashattntile_amd import PagedKVCache, paged_decode_attention, paged_decode_attention_fp8
+from flashattntile_amd.kernels.decode import paged_decode_launch
+from oracle import quant_ref
+from oracle.reference import ref_attention_paged
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ODD_LENS = [1, 17, 255, 1000]
+GQA = [(8, 8), (8, 2), (8, 1), (32, 8), (32, 1)]
+
+
+def _case(lens, h, hk, d, P, dtype, seed=0):
+    k, v, pt, sl = make_paged(lens, hk, d, P, dtype, seed=seed, device=DEV)
+    q = make_query(len(lens), h, d, dtype, seed=seed + 1, device=DEV)
+    return q, PagedKVCache(k, v, pt, sl, P)
+
+
+def _ref32(q, cache, scale=None):
+    return ref_attention_paged(q.cpu(), cache.k_cache.cpu(), cache.v_cache.cpu(), cache.page_table.cpu(),
+                               cache.seq_lens.cpu(), softmax_scale=scale, return_fp32=True)
+
+
+@pytest.mark.parametrize("split_k", [1, 4])
+@pytest.mark.parametrize("page_size", [16, 32])
+@pytest.mark.parametrize("h,hk", GQA)
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_matches_oracle(dtype, d, h, hk, page_size, split_k):
+    label = f"decode {dtype} D{d} H{h}/{hk} P{page_size} sk{split_k}"
+    print(label, flush=True)
+    q, cache = _case(ODD_LENS, h, hk, d, page_size, dtype, seed=d + h + hk)
+    out = paged_decode_attention(q, cache, config={"split_k": split_k})
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == dtype
+    assert_parity(out, _ref32(q, cache), label=label)
+
+
+@pytest.mark.parametrize("page_size", [4, 8, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_page_sizes(dtype, page_size):
+    label = f"decode pages {dtype} P{page_size}"
+    print(label, flush=True)
+    d = 128 if page_size >= 8 else 128
+    lens = [3, 64, 65, 300]
+    q, cache = _case(lens, 32, 8, d, page_size, dtype, seed=page_size)
+    for split_k in (1, 3):
+        out = paged_decode_attention(q, cache, config={"split_k": split_k})
+        torch.cuda.synchronize()
+        assert_parity(out, _ref32(q, cache), label=f"{label} sk{split_k}")
+
+
+def test_decode_more_splits_than_pages():
+    """Empty partitions must contribute nothing (reference test_decode.py:132-139)."""
+    print("decode split 16 > pages", flush=True)
+    q, cache = _case([8, 20], 4, 2, 64, 16, torch.float16, seed=24)
+    out = paged_decode_attention(q, cache, config={"split_k": 16})
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label="split16")
+
+
+def test_split_k_agreement_and_softmax_scale():
+    print("decode split agreement", flush=True)
+    lens = [1, 17, 255, 1000, 4096, 333]
+    q, cache = _case(lens, 32, 8, 128, 16, torch.float16, seed=22)
+    ref = _ref32(q, cache, scale=0.05)
+    outs = {}
+    for s in (1, 2, 5, 8, 16, 64):
+        outs[s] = paged_decode_attention(q, cache, softmax_scale=0.05, config={"split_k": s})
+    torch.cuda.synchronize()
+    for s, o in outs.items():
+        assert_parity(o, ref, label=f"scale0.05 sk{s}")
+        assert (o.float() - outs[1].float()).abs().max().item() <= 2e-3
+
+
+def _quant_case(lens, h, hk, d, P, qdtype, mode, seed):
+    k, v, pt, sl = make_paged(lens, hk, d, P, torch.float32, seed=seed, device="cpu")
+    qk, sk = quant_ref.quantize_pages(k, mode)
+    qv, sv = quant_ref.quantize_pages(v, mode)
+    q = make_query(len(lens), h, d, qdtype, seed=seed + 1, device=DEV)
+    cache = PagedKVCache(qk.to(DEV), qv.to(DEV), pt.to(DEV), sl.to(DEV), P)
+    deq_k = quant_ref.dequantize_pages(qk, sk, qdtype)
+    deq_v = quant_ref.dequantize_pages(qv, sv, qdtype)
+    ref = ref_attention_paged(q.cpu(), deq_k, deq_v, pt, sl, return_fp32=True)
+    return q, cache, {"k": sk.to(DEV), "v": sv.to(DEV)}, ref
+
+
+@pytest.mark.parametrize("split_k", [1, 4])
+@pytest.mark.parametrize("h,hk", [(8, 2), (32, 8), (8, 8), (32, 1)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+def test_quant_decode_matches_dequantized_oracle(mode, qdtype, d, h, hk, split_k):
+    label = f"quant {mode} {qdtype} D{d} H{h}/{hk} sk{split_k}"
+    print(label, flush=True)
+    q, cache, scales, ref = _quant_case(ODD_LENS, h, hk, d, 16, qdtype, mode, seed=13 + d)
+    out = paged_decode_attention_fp8(q, cache, scales, config={"split_k": split_k})
+    torch.cuda.synchronize()
+    assert out.dtype == qdtype
+    assert_parity(out, ref, label=label)
+
+
+def test_permuted_pool_is_bit_identical():
+    """Relocating pages (and remapping the table) must not change one bit."""
+    print("decode permutation invariance", flush=True)
+    q, cache = _case([700, 1, 4096, 129], 32, 8, 128, 16, torch.bfloat16, seed=31)
+    out = paged_decode_attention(q, cache, config={"split_k": 4})
+    g = torch.Generator().manual_seed(5)
+    perm = torch.randperm(cache.num_pages, generator=g).to(DEV)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(cache.num_pages, device=DEV)
+    moved = PagedKVCache(cache.k_cache[perm].contiguous(), cache.v_cache[perm].contiguous(),
+                         inv[cache.page_table.long()].to(torch.int32), cache.seq_lens, cache.page_size)
+    out2 = paged_decode_attention(q, moved, config={"split_k": 4})
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_baseline_config_b32_ctx4096():
+    """fp16, B32, ctx 4096, 32/8 heads, D128, page 16."""
+    print("decode B32 ctx4096", flush=True)
+    q, cache = _case([4096] * 32, 32, 8, 128, 16, torch.float16, seed=1)
+    for split_k in (1, 4, 8):
+        out = paged_decode_attention(q, cache, config={"split_k": split_k})
+        torch.cuda.synchronize()
+        assert_parity(out, _ref32(q, cache), label=f"B32 ctx4096 sk{split_k}")
+
+
+def test_long_context_and_skewed_batch():
+    """B1 ctx 131072 (split 16) and 64 log-uniform lengths."""
+    print("decode ctx131072", flush=True)
+    q, cache = _case([131072], 32, 8, 128, 16, torch.float16, seed=2)
+    out = paged_decode_attention(q, cache, config={"split_k": 16})
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label="ctx131072 sk16")
+    print("decode skewed batch", flush=True)
+    g = torch.Generator().manual_seed(64)
+    lens = [int(math.exp(x)) for x in (torch.rand(64, generator=g) * (math.log(65536) - math.log(16))
+                                        + math.log(16)).tolist()]
+    q, cache = _case(lens, 32, 8, 128, 16, torch.float16, seed=3)
+    out = paged_decode_attention(q, cache)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label="skewed64")
+
+
+@pytest.mark.parametrize("h,hk,d,P", [(32, 1, 128, 16), (32, 8, 64, 16), (32, 8, 128, 32), (32, 8, 128, 64)])
+def test_stress_variants(h, hk, d, P):
+    label = f"stress H{h}/{hk} D{d} P{P}"
+    print(label, flush=True)
+    q, cache = _case([16, 1000, 8191, 3000], h, hk, d, P, torch.float16, seed=h + hk + d + P)
+    out = paged_decode_attention(q, cache)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label=label)
+
+
+def test_launch_reuses_buffers():
+    """paged_decode_launch with caller-owned out/workspace (no allocation)."""
+    print("decode launch reuse", flush=True)
+    from flashattntile_amd import _hip
+    q, cache = _case([100, 2000], 32, 8, 128, 16, torch.float16, seed=40)
+    out = torch.empty_like(q)
+    ws = torch.empty(_hip.decode_workspace_bytes(2, 32, 128, 8), dtype=torch.uint8, device=DEV)
+    r = paged_decode_launch(q, cache, 128 ** -0.5, 8, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert r.data_ptr() == out.data_ptr()
+    assert_parity(out, _ref32(q, cache), label="launch reuse")
+
+
+def test_native_library_is_the_path():
+    import flashattntile_amd._hip as hip
+    assert hip.is_loaded(), hip.load_error()
+    with open("/proc/self/maps") as fh:
+        assert "libfat_hip.so" in fh.read()

@@ -1,0 +1,100 @@
+"""Quantisation format: product helpers vs the oracle restatement and KATs."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from flashattntile_amd import quant
+from flashattntile_amd.paging import allocate, append_tokens
+from oracle import quant_ref
+
+FP8 = getattr(torch, "float8_e4m3fn", None)
+
+
+def test_fp8_table_matches_torch_exhaustively():
+    """All 256 OCP e4m3fn codes: bit-field decoding == torch's conversion."""
+    table = quant_ref.fp8_table()
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(FP8).float()
+    same = (table == codes) | (torch.isnan(table) & torch.isnan(codes))
+    assert bool(same.all())
+    assert table[0x7E].item() == 448.0 and table[0x08].item() == 2.0 ** -6 and table[0x01].item() == 2.0 ** -9
+    assert math.isnan(table[0x7F].item()) and math.isnan(table[0xFF].item())
+
+
+def test_int8_kats():
+    # One page, one head: absmax 2.54 -> scale 0.02; values map to integers.
+    x = torch.tensor([2.54, -1.27, 0.01, 0.03, -0.05, 0.0, 0.5, -2.54]).view(1, 8, 1, 1)
+    q, s = quant_ref.quantize_pages(x, "int8")
+    assert s.shape == (1, 1)
+    assert abs(s.item() - 2.54 / 127) < 1e-9
+    # 0.01/0.02 = 0.5 -> 0 (half to even), 0.03/0.02 = 1.5 -> 2, -0.05/0.02 = -2.5 -> -2
+    assert q.view(-1).tolist() == [127, -64, 0, 2, -2, 0, 25, -127]
+    # All-zero page: scale floors at 1e-8 and everything quantises to 0.
+    qz, sz = quant_ref.quantize_pages(torch.zeros(2, 4, 3, 2), "int8")
+    assert torch.all(sz == 1e-8) and torch.all(qz == 0)
+
+
+def test_fp8_kats():
+    x = torch.tensor([448.0, -448.0, 1.0, 0.0]).view(1, 4, 1, 1) * 0.5
+    q, s = quant_ref.quantize_pages(x, "float8_e4m3fn")
+    assert abs(s.item() - 224.0 / 448.0) < 1e-12
+    assert q.view(torch.uint8).view(-1).tolist() == [0x7E, 0xFE, 0x38, 0x00]  # 448, -448, 1.0, 0
+
+
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_product_quantise_equals_oracle(mode, out_dtype):
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(6, 16, 2, 64, generator=g).to(torch.float16)
+    v = torch.randn(6, 16, 2, 64, generator=g).to(torch.float16)
+    qk, qv, sk, sv, info = quant.quantize_kv_pages(k, v, mode=mode)
+    ok, osk = quant_ref.quantize_pages(k, mode)
+    ov, osv = quant_ref.quantize_pages(v, mode)
+    assert info["mode"] == mode and sk.shape == (6, 2)
+    assert torch.equal(qk.view(torch.uint8), ok.view(torch.uint8))
+    assert torch.equal(qv.view(torch.uint8), ov.view(torch.uint8))
+    assert torch.equal(sk, osk) and torch.equal(sv, osv)
+    dk, dv = quant.dequantize_kv_pages(qk, qv, sk, sv, out_dtype=out_dtype)
+    assert torch.equal(dk, quant_ref.dequantize_pages(ok, osk, out_dtype))
+    assert torch.equal(dv, quant_ref.dequantize_pages(ov, osv, out_dtype))
+    # Error bound of the format: |x - deq| <= scale/2 (int8) or half an fp8 ulp
+    # (<= 16 * scale at the top binade), plus the output dtype's rounding.
+    err = (dk.float() - k.float()).abs()
+    rel = {torch.float16: 1e-3, torch.bfloat16: 4e-3, torch.float32: 1e-6}[out_dtype]
+    bound = sk[:, None, :, None] * (0.5 if mode == "int8" else 16.0) + rel * k.float().abs()
+    assert torch.all(err <= bound)
+
+
+def test_quantize_cache_roundtrip_shapes():
+    cache = allocate(2, 20, 2, 16, 16, dtype=torch.float32)
+    for _ in range(20):
+        append_tokens(cache, torch.randn(2, 2, 16), torch.randn(2, 2, 16))
+    qc, scales = quant.quantize_cache(cache, mode="int8")
+    assert qc.k_cache.dtype == torch.int8 and scales.k.shape == (cache.num_pages, 2)
+    assert scales.as_dict()["granularity"] == "per_page_per_head"
+    deq = quant.dequantize_cache(qc, scales, out_dtype=torch.float32)
+    assert deq.k_cache.shape == cache.k_cache.shape
+    assert (deq.k_cache - cache.k_cache).abs().max() <= scales.k.max() / 2 + 1e-6
+
+
+def test_bytes_per_token_kats():
+    """results/numerics.json:43-47 of the reference: 4100 vs 2052 bytes."""
+    assert quant.kv_bytes_per_token(8, 128, "fp16", 16) == 4100.0
+    assert quant.kv_bytes_per_token(8, 128, "int8", 16) == 2052.0
+    assert quant.kv_bytes_per_token(8, 128, "fp8", 16) == 2052.0
+    assert quant.kv_bytes_per_token(8, 128, "int8", 16) < quant.kv_bytes_per_token(8, 128, "fp16", 16) / 1.9
+
+
+def test_modes_and_errors():
+    assert "int8" in quant.available_quant_modes()
+    assert quant.default_quant_mode() in ("int8", "float8_e4m3fn")
+    with pytest.raises(ValueError, match="unknown quantisation mode"):
+        quant.quantize_kv_pages(torch.zeros(1, 2, 1, 2), torch.zeros(1, 2, 1, 2), mode="int4")
+    with pytest.raises(ValueError, match="float cache"):
+        quant.quantize_kv_pages(torch.zeros(1, 2, 1, 2, dtype=torch.int8), torch.zeros(1, 2, 1, 2, dtype=torch.int8))
+    with pytest.raises(ValueError, match="scale_k shape"):
+        quant.dequantize_kv_pages(torch.zeros(2, 2, 1, 2, dtype=torch.int8), torch.zeros(2, 2, 1, 2, dtype=torch.int8),
+                                  torch.ones(3, 1), torch.ones(3, 1))
