@@ -1,7 +1,381 @@
-// prefill.hip -- placeholder until the MFMA kernel lands.
+// prefill.hip -- packed varlen flash-attention forward for gfx950 (CDNA4 MFMA).
+//
+// Behaviour follows flashattn_tile/kernels/prefill.py:35-138
+// (_fwd_varlen_kernel): per (query block, query head, sequence) it streams
+// K/V blocks, keeps a running max / sum / fp32 accumulator (online softmax),
+// applies bottom-right causal masking (query i sees key j iff
+// j <= i + kv_len - q_len) and writes q.dtype.
+//
+// MI355X design (not a translation of the Triton program):
+//   * workgroup = 4 waves x 32 query rows (BM = 128); K/V blocks of BN = 64
+//     keys are staged in LDS in their natural [key][dim] layout and shared by
+//     the 4 waves; the next block is prefetched into registers while the
+//     current one is computed;
+//   * scores are computed transposed, S^T = K Q^T, with
+//     v_mfma_f32_32x32x16_{f16,bf16}: the accumulator then holds one query
+//     per lane (column) and 32 keys per lane pair, so the softmax row max /
+//     sum need a single lane^32 exchange and the O accumulator is rescaled
+//     lane-locally;
+//   * O^T = V^T P^T: P^T is the B operand straight from the S^T accumulator
+//     registers (the key order inside an MFMA k-step is chosen to match the
+//     accumulator layout), and V^T comes from LDS through
+//     ds_read_b64_tr_b16, so V never needs a transposed copy;
+//   * P is rounded to the input dtype for the PV product (as
+//     prefill.py:128 does); for bf16 it is split into hi + lo bf16 parts and
+//     both are multiplied, which keeps the result within fp32-level error of
+//     the fp32 reference;
+//   * exp is 2^(x * log2 e) on v_exp_f32;
+//   * the 1-D grid walks query blocks longest-first (causal balance) and
+//     assigns the query heads that share a KV head to the same XCD
+//     (workgroup id mod 8), so K/V blocks are reused from that XCD's L2.
 #include "fat_common.h"
-extern "C" size_t fat_prefill_workspace_bytes(int32_t, int32_t, int32_t) { return 0; }
-extern "C" int fat_prefill_varlen(const fat_prefill_args*, void*) {
-  fat_host::set_error("fat_prefill_varlen: not built yet");
-  return FAT_E_UNSUPPORTED;
+
+namespace fat {
+
+struct PrefillParams {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  uint8_t* out;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // element strides
+  int32_t B, H, Hkv, group, nqb;
+  float scale_log2;
+};
+
+template <typename T> struct Mfma;
+template <> struct Mfma<F16> {
+  static __device__ __forceinline__ f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  }
+};
+template <> struct Mfma<BF16> {
+  static __device__ __forceinline__ f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+  }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Transposed 64-bit LDS read: inside each 16-lane group, lane l receives
+// element (l % 4) of the 4-element row addressed by lane 4c + l/4, for
+// c = 0..3 (gfx950 ds_read_b64_tr_b16).
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+constexpr int kBM = 128;
+constexpr int kBN = 64;
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
+  constexpr int KS = D / 16;        // MFMA k-steps of S^T over the head dim
+  constexpr int DB = D / 32;        // 32-row blocks of O^T
+  constexpr int K_RS = D + 8;       // LDS row strides (elements), chosen to
+  constexpr int V_RS = D + 32;      // spread 16-byte / transposed reads over banks
+  constexpr int CPR = D / 8;        // 16-byte chunks per K/V row
+  constexpr int LOADS = kBN * CPR / 256;
+  constexpr bool SPLIT_P = std::is_same<T, BF16>::value;
+  static_assert(LOADS >= 1, "tile too small");
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * K_RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * V_RS];
+
+  // ---- work item: longest query blocks first; heads sharing a KV head
+  // ---- land on the same XCD (consecutive ids go to consecutive XCDs).
+  const int per = p.B * p.H;
+  const int outer = blockIdx.x / per;
+  const int rem = blockIdx.x - outer * per;
+  const int b = rem / p.H;
+  const int j = rem - b * p.H;
+  const int kvh = j % p.Hkv;
+  const int h = kvh * p.group + j / p.Hkv;
+  const int mb = p.nqb - 1 - outer;
+
+  const int q_start = p.cu_q[b];
+  const int q_len = p.cu_q[b + 1] - q_start;
+  const int k_start = p.cu_k[b];
+  const int kv_len = p.cu_k[b + 1] - k_start;
+  if (mb * kBM >= q_len) return;  // uniform over the workgroup
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5;   // k-group of the MFMA operands
+  const int li = lane & 31;  // query column of this lane
+  const int shift = kv_len - q_len;
+  const int row0 = mb * kBM + w * 32;  // first query row of this wave
+  const int my_row = row0 + li;
+
+  // Q^T operand (B of S^T = K Q^T): lane holds Q[my_row][16 ks + 8 g + 0..7].
+  u32x4 qf[KS];
+  {
+    const int qr = min(my_row, q_len - 1);
+    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+  }
+
+  int hi = kv_len;
+  if (CAUSAL) hi = min(kv_len, (mb + 1) * kBM + shift);
+  const int n_tiles = hi > 0 ? (hi + kBN - 1) / kBN : 0;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  u32x4 kreg[LOADS], vreg[LOADS];
+  auto gload = [&](int tile) {
+    const int n0 = tile * kBN;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int cid = tid + 256 * u;
+      const int key = cid / CPR;
+      const int col = cid % CPR;
+      const int kk = k_start + min(n0 + key, kv_len - 1);
+      kreg[u] = *reinterpret_cast<const u32x4*>(p.k + 2 * ((int64_t)kk * p.k_st + (int64_t)kvh * p.k_sh + 8 * col));
+      vreg[u] = *reinterpret_cast<const u32x4*>(p.v + 2 * ((int64_t)kk * p.v_st + (int64_t)kvh * p.v_sh + 8 * col));
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int cid = tid + 256 * u;
+      const int key = cid / CPR;
+      const int col = cid % CPR;
+      *reinterpret_cast<u32x4*>(&Ks[key * K_RS + 8 * col]) = kreg[u];
+      *reinterpret_cast<u32x4*>(&Vs[key * V_RS + 8 * col]) = vreg[u];
+    }
+  };
+
+  // Lane roles of the transposed V reads (see lds_read_tr16).
+  const int tr_c = (lane & 15) >> 2;
+  const int tr_j = lane & 3;
+  const int tr_G = lane >> 4;
+  const int tr_row = 4 * (tr_G >> 1) + tr_c;      // + 32 jb + 16 t (+ 8)
+  const int tr_col = 16 * (tr_G & 1) + 4 * tr_j;  // + 32 db
+
+  if (n_tiles > 0) gload(0);
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    __syncthreads();
+    lstore();
+    __syncthreads();
+    if (tile + 1 < n_tiles) gload(tile + 1);
+    const int n0 = tile * kBN;
+
+    // ---- S^T = K Q^T for two 32-key blocks ----
+    f32x16 s[2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Ks[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
+        s[jb] = Mfma<T>::mma(a, qf[ks], s[jb]);
+      }
+    }
+
+    // ---- online softmax for query my_row (lane pair li, li + 32) ----
+    const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[jb][r] * p.scale_log2;
+        if (need_mask) {
+          const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
+          const bool ok = key < kv_len && (!CAUSAL || key <= my_row + shift);
+          x = ok ? x : -INFINITY;
+        }
+        s[jb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = xor32<OpMax>(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float ls = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = fast_exp2(s[jb][r] - m_new);
+        s[jb][r] = e;
+        ls += e;
+      }
+    l_run = l_run * alpha + ls;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+
+    // ---- P^T operands (k-step t of key block jb uses accumulator regs 8t..8t+7) ----
+    u32x4 pf[2][2];
+    u32x4 pl[2][2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float x0 = s[jb][8 * t + 2 * e2];
+          const float x1 = s[jb][8 * t + 2 * e2 + 1];
+          const u32 hp = Pair<T>::pack(x0, x1);
+          pf[jb][t][e2] = hp;
+          if constexpr (SPLIT_P) {
+            pl[jb][t][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+          }
+        }
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int vrow = jb * 32 + 16 * t + tr_row;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const uint16_t* vp = &Vs[vrow * V_RS + 32 * db + tr_col];
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
+          const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
+          acc[db] = Mfma<T>::mma(a, pf[jb][t], acc[db]);
+          if constexpr (SPLIT_P) acc[db] = Mfma<T>::mma(a, pl[jb][t], acc[db]);
+        }
+      }
+  }
+
+  // ---- epilogue: O = O^T / l, lane writes 4 consecutive dims per store ----
+  const float l_tot = xor32<OpAdd>(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (my_row < q_len) {
+    uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * db + 4 * g + 8 * rr;
+        u32x2 pk;
+        pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
+        pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + 2 * d0) = pk;
+      }
+  }
+}
+
+}  // namespace fat
+
+// ===========================================================================
+// Host side
+// ===========================================================================
+namespace {
+
+template <typename T, int D>
+int launch_prefill_t(const fat::PrefillParams& prm, bool causal, dim3 grid, hipStream_t stream) {
+  if (causal) {
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, true>), grid, dim3(256), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, false>), grid, dim3(256), 0, stream, prm);
+  }
+  return fat_host::launch_status("prefill_kernel");
+}
+
+}  // namespace
+
+extern "C" size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads, int32_t head_dim) {
+  (void)total_k;
+  (void)num_kv_heads;
+  (void)head_dim;
+  return 0;  // V is transposed on the fly (ds_read_b64_tr_b16); no staging copy
+}
+
+extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
+  fat_host::clear_error();
+  if (!a) {
+    fat_host::set_error("fat_prefill_varlen: args is NULL");
+    return FAT_E_INVALID;
+  }
+  if (!a->q || !a->k || !a->v || !a->cu_seqlens_q || !a->cu_seqlens_k || !a->out) {
+    fat_host::set_error("fat_prefill_varlen: a required pointer is NULL");
+    return FAT_E_INVALID;
+  }
+  if (a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->total_q < 0 || a->total_k < 0) {
+    fat_host::set_error("fat_prefill_varlen: batch and head counts must be positive");
+    return FAT_E_INVALID;
+  }
+  if (a->num_heads % a->num_kv_heads != 0) {
+    fat_host::set_error("fat_prefill_varlen: num_heads %d must be divisible by num_kv_heads %d", a->num_heads,
+                        a->num_kv_heads);
+    return FAT_E_INVALID;
+  }
+  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16) {
+    fat_host::set_error("fat_prefill_varlen: dtype must be fp16 or bf16");
+    return FAT_E_UNSUPPORTED;
+  }
+  const int D = a->head_dim;
+  if (D != 64 && D != 128) {
+    fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (64 or 128)", D);
+    return FAT_E_UNSUPPORTED;
+  }
+  if (a->max_seqlen_q < 0 || a->max_seqlen_k < 0) {
+    fat_host::set_error("fat_prefill_varlen: max_seqlen must be non-negative");
+    return FAT_E_INVALID;
+  }
+  const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)(2 * a->q_stride_t) |
+                            (uintptr_t)(2 * a->q_stride_h) | (uintptr_t)(2 * a->k_stride_t) |
+                            (uintptr_t)(2 * a->k_stride_h) | (uintptr_t)(2 * a->v_stride_t) |
+                            (uintptr_t)(2 * a->v_stride_h);
+  const uintptr_t align8 = (uintptr_t)a->out | (uintptr_t)(2 * a->out_stride_t) | (uintptr_t)(2 * a->out_stride_h);
+  if ((align16 & 15) || (align8 & 7)) {
+    fat_host::set_error("fat_prefill_varlen: q/k/v rows must be 16-byte aligned and out rows 8-byte aligned");
+    return FAT_E_INVALID;
+  }
+  if (a->max_seqlen_q == 0 || a->total_q == 0) return FAT_OK;  // nothing to compute
+
+  fat::PrefillParams prm{};
+  prm.q = static_cast<const uint8_t*>(a->q);
+  prm.k = static_cast<const uint8_t*>(a->k);
+  prm.v = static_cast<const uint8_t*>(a->v);
+  prm.cu_q = a->cu_seqlens_q;
+  prm.cu_k = a->cu_seqlens_k;
+  prm.out = static_cast<uint8_t*>(a->out);
+  prm.q_st = a->q_stride_t;
+  prm.q_sh = a->q_stride_h;
+  prm.k_st = a->k_stride_t;
+  prm.k_sh = a->k_stride_h;
+  prm.v_st = a->v_stride_t;
+  prm.v_sh = a->v_stride_h;
+  prm.o_st = a->out_stride_t;
+  prm.o_sh = a->out_stride_h;
+  prm.B = a->batch;
+  prm.H = a->num_heads;
+  prm.Hkv = a->num_kv_heads;
+  prm.group = a->num_heads / a->num_kv_heads;
+  prm.nqb = (a->max_seqlen_q + fat::kBM - 1) / fat::kBM;
+  prm.scale_log2 = a->softmax_scale * fat::kLog2e;
+  const int64_t n = (int64_t)prm.nqb * a->batch * a->num_heads;
+  if (n > 0x7fffffff) {
+    fat_host::set_error("fat_prefill_varlen: too many query blocks (%lld)", (long long)n);
+    return FAT_E_UNSUPPORTED;
+  }
+  const dim3 grid((unsigned)n);
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const bool causal = a->causal != 0;
+  if (a->dtype == FAT_DTYPE_F16) {
+    return D == 128 ? launch_prefill_t<fat::F16, 128>(prm, causal, grid, stream)
+                    : launch_prefill_t<fat::F16, 64>(prm, causal, grid, stream);
+  }
+  return D == 128 ? launch_prefill_t<fat::BF16, 128>(prm, causal, grid, stream)
+                  : launch_prefill_t<fat::BF16, 64>(prm, causal, grid, stream);
 }
