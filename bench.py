@@ -40,7 +40,21 @@ def _parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--split-k", type=int, default=0, help="force split_k (0 = pick during warm-up)")
     ap.add_argument("--waves", type=int, default=0, help="force waves per workgroup (0 = pick)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 1 GiB copy kernel (torch.neg on fp32) three times, the known-size "
+                         "reference that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by")
     return ap.parse_args()
+
+
+def copy_calibration(device, nbytes=1 << 30):
+    """A plain elementwise copy of known size: reads and writes ``nbytes``."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    return nbytes
 
 
 def _decode_inputs(batch, ctx, hq, hkv, d, page, dtype, seed, device, copies=2):
@@ -211,6 +225,10 @@ def main():
         print(f"bench.py: HIP library unavailable: {_hip.load_error()}", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calibration:
+        n = copy_calibration(device)
+        print(f"# copy calibration: 3 x torch.neg over {n} bytes read + {n} bytes written", file=sys.stderr,
+              flush=True)
     dec = bench_decode(args, device)
     print(f"# decode: {dec['gbs']:.1f} GB/s ({dec['ms'] * 1e3:.1f} us/step, split_k={dec['split_k']}, "
           f"waves={dec['waves_per_group']})", file=sys.stderr, flush=True)

@@ -71,9 +71,16 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 
 constexpr int kBM = 128;
 constexpr int kBN = 64;
+// A row's running max is only moved (and O rescaled) when a tile's max
+// exceeds it by more than this many log2 units; p = 2^(x - m) then stays
+// below 2^kLazy, which fp16/bf16 P and the fp32 sums hold exactly as well.
+constexpr float kLazy = 8.0f;
 
-template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
+// POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
+// is folded into the exponent's fma; otherwise scores are scaled first.
+template <typename T, int D, bool CAUSAL, bool POS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;        // MFMA k-steps of S^T over the head dim
   constexpr int DB = D / 32;        // 32-row blocks of O^T
   constexpr int K_RS = D + 8;       // LDS row strides (elements), chosen to
@@ -83,8 +90,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   constexpr bool SPLIT_P = std::is_same<T, BF16>::value;
   static_assert(LOADS >= 1, "tile too small");
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * K_RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * V_RS];
+  // Two K/V buffers: tile t+1 is written while tile t is read, so one
+  // workgroup barrier per tile suffices.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * V_RS];
 
   // ---- work item: longest query blocks first; heads sharing a KV head
   // ---- land on the same XCD (consecutive ids go to consecutive XCDs).
@@ -111,6 +120,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   const int shift = kv_len - q_len;
   const int row0 = mb * kBM + w * 32;  // first query row of this wave
   const int my_row = row0 + li;
+  const float c = p.scale_log2;
 
   // Q^T operand (B of S^T = K Q^T): lane holds Q[my_row][16 ks + 8 g + 0..7].
   u32x4 qf[KS];
@@ -130,7 +140,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-  float m_run = -INFINITY;
+  float m_run = -INFINITY;  // scaled (log2) units
   float l_run = 0.f;
 
   u32x4 kreg[LOADS], vreg[LOADS];
@@ -146,14 +156,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       vreg[u] = *reinterpret_cast<const u32x4*>(p.v + 2 * ((int64_t)kk * p.v_st + (int64_t)kvh * p.v_sh + 8 * col));
     }
   };
-  auto lstore = [&]() {
+  auto lstore = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
       const int key = cid / CPR;
       const int col = cid % CPR;
-      *reinterpret_cast<u32x4*>(&Ks[key * K_RS + 8 * col]) = kreg[u];
-      *reinterpret_cast<u32x4*>(&Vs[key * V_RS + 8 * col]) = vreg[u];
+      *reinterpret_cast<u32x4*>(&Ks[buf][key * K_RS + 8 * col]) = kreg[u];
+      *reinterpret_cast<u32x4*>(&Vs[buf][key * V_RS + 8 * col]) = vreg[u];
     }
   };
 
@@ -164,13 +174,23 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
   const int tr_row = 4 * (tr_G >> 1) + tr_c;      // + 32 jb + 16 t (+ 8)
   const int tr_col = 16 * (tr_G & 1) + 4 * tr_j;  // + 32 db
 
-  if (n_tiles > 0) gload(0);
+  if (n_tiles > 0) {
+    gload(0);
+    lstore(0);
+    if (n_tiles > 1) gload(1);
+  }
   for (int tile = 0; tile < n_tiles; ++tile) {
+    const int buf = tile & 1;
+    // Tile `tile` is in Ks/Vs[buf]; every wave is done with tile - 1, whose
+    // buffer now takes tile + 1 (already in registers).
     __syncthreads();
-    lstore();
-    __syncthreads();
-    if (tile + 1 < n_tiles) gload(tile + 1);
+    if (tile + 1 < n_tiles) {
+      lstore(buf ^ 1);
+      if (tile + 2 < n_tiles) gload(tile + 2);
+    }
     const int n0 = tile * kBN;
+    const uint16_t* Kb = Ks[buf];
+    const uint16_t* Vb = Vs[buf];
 
     // ---- S^T = K Q^T for two 32-key blocks ----
     f32x16 s[2];
@@ -180,7 +200,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&Ks[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Kb[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
         s[jb] = Mfma<T>::mma(a, qf[ks], s[jb]);
       }
     }
@@ -192,7 +212,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float x = s[jb][r] * p.scale_log2;
+        float x = POS ? s[jb][r] : s[jb][r] * c;
         if (need_mask) {
           const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
           const bool ok = key < kv_len && (!CAUSAL || key <= my_row + shift);
@@ -202,23 +222,31 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
         mx = fmaxf(mx, x);
       }
     mx = xor32<OpMax>(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
+    if (POS) mx *= c;  // exact: rounding is monotonic and c > 0
+    // Lazy rescale: keep m_run unless this tile's max exceeds it by kLazy.
+    float alpha = 1.f;
+    if (mx > m_run + kLazy) {
+      alpha = fast_exp2(m_run - mx);
+      m_run = mx;
+    }
+    const float cm = POS ? c : 1.f;
+    const float nm = -m_run;
     float ls = 0.f;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(s[jb][r] - m_new);
+        const float e = fast_exp2(__builtin_fmaf(s[jb][r], cm, nm));
         s[jb][r] = e;
         ls += e;
       }
-    l_run = l_run * alpha + ls;
+    l_run = __builtin_fmaf(l_run, alpha, ls);
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+      for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+    }
 
     // ---- P^T operands (k-step t of key block jb uses accumulator regs 8t..8t+7) ----
     u32x4 pf[2][2];
@@ -246,7 +274,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
         const int vrow = jb * 32 + 16 * t + tr_row;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const uint16_t* vp = &Vs[vrow * V_RS + 32 * db + tr_col];
+          const uint16_t* vp = &Vb[vrow * V_RS + 32 * db + tr_col];
           const u32x2 lo = lds_read_tr16(vp);
           const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
           const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
@@ -281,13 +309,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
 // ===========================================================================
 namespace {
 
+template <typename T, int D, bool CAUSAL>
+void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
+  if (pos) {
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true>), grid, dim3(256), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false>), grid, dim3(256), 0, stream, prm);
+  }
+}
+
 template <typename T, int D>
 int launch_prefill_t(const fat::PrefillParams& prm, bool causal, dim3 grid, hipStream_t stream) {
-  if (causal) {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, true>), grid, dim3(256), 0, stream, prm);
-  } else {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, false>), grid, dim3(256), 0, stream, prm);
-  }
+  const bool pos = prm.scale_log2 > 0.f;
+  if (causal) launch_prefill_c<T, D, true>(prm, pos, grid, stream);
+  else launch_prefill_c<T, D, false>(prm, pos, grid, stream);
   return fat_host::launch_status("prefill_kernel");
 }
 
