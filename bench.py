@@ -38,6 +38,10 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--legs", default="decode,prefill,cpu",
+                    help="comma list of decode, prefill, cpu (the JSON line needs decode)")
+    ap.add_argument("--tune", action="store_true",
+                    help="time a few split_k / waves candidates in warm-up and keep the fastest")
     ap.add_argument("--split-k", type=int, default=0, help="force split_k (0 = pick during warm-up)")
     ap.add_argument("--waves", type=int, default=0, help="force waves per workgroup (0 = pick)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -89,7 +93,7 @@ def _time_steps(fn, steps, warmup, stream):
 
 def bench_decode(args, device):
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged
+    from flashattntile_amd.autotune import bytes_decode_paged, decode_split_k
 
     B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
     dtype = torch.float16
@@ -108,14 +112,15 @@ def bench_decode(args, device):
                               waves_per_group=waves)
         return step
 
-    if args.split_k or args.waves:
-        cands = [(args.split_k or 1, args.waves or 0)]
-    else:
+    if args.tune:
         cands = [(s, w) for s in (1, 2, 3, 4, 8) for w in (4, 8)]
+    else:
+        cands = [(args.split_k or decode_split_k(B, HQ, HKV, (CTX + P - 1) // P), args.waves or 0)]
     tuning = {}
-    for cand in cands:
-        tuning[cand] = _time_steps(make(*cand), max(5, args.warmup // 4), 2, stream)
-    s, w = min(tuning, key=tuning.get)
+    if len(cands) > 1:
+        for cand in cands:
+            tuning[cand] = _time_steps(make(*cand), max(5, args.warmup // 4), 2, stream)
+    s, w = min(tuning, key=tuning.get) if tuning else cands[0]
     torch.cuda.synchronize()
     ms = _time_steps(make(s, w), args.steps, args.warmup, stream)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -229,11 +234,18 @@ def main():
         n = copy_calibration(device)
         print(f"# copy calibration: 3 x torch.neg over {n} bytes read + {n} bytes written", file=sys.stderr,
               flush=True)
-    dec = bench_decode(args, device)
-    print(f"# decode: {dec['gbs']:.1f} GB/s ({dec['ms'] * 1e3:.1f} us/step, split_k={dec['split_k']}, "
-          f"waves={dec['waves_per_group']})", file=sys.stderr, flush=True)
+    legs = set(args.legs.split(","))
+    if args.no_prefill:
+        legs.discard("prefill")
+    if args.no_cpu_baseline:
+        legs.discard("cpu")
+    dec = None
+    if "decode" in legs:
+        dec = bench_decode(args, device)
+        print(f"# decode: {dec['gbs']:.1f} GB/s ({dec['ms'] * 1e3:.1f} us/step, split_k={dec['split_k']}, "
+              f"waves={dec['waves_per_group']})", file=sys.stderr, flush=True)
     pre = None
-    if not args.no_prefill:
+    if "prefill" in legs:
         try:
             pre = bench_prefill(args, device)
             print(f"# prefill seq8192: {pre['tflops']:.1f} TFLOP/s ({pre['ms']:.3f} ms)", file=sys.stderr,
@@ -241,9 +253,11 @@ def main():
         except RuntimeError as exc:  # prefill kernel not available in this build
             pre = {"error": str(exc)}
     cpu = None
-    if not args.no_cpu_baseline:
+    if "cpu" in legs:
         cpu = cpu_baseline_decode()
         print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} cores", file=sys.stderr, flush=True)
+    if dec is None:
+        return
 
     workload = "decode_fp16_b32_ctx4096_h32_kv8_d128_p16"
     line = {

@@ -71,6 +71,9 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 
 constexpr int kBM = 128;
 constexpr int kBN = 64;
+// Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
+constexpr int kBufFlags = 0x00020000;
+
 // A row's running max is only moved (and O rescaled) when a tile's max
 // exceeds it by more than this many log2 units; p = 2^(x - m) then stays
 // below 2^kLazy, which fp16/bf16 P and the fp32 sums hold exactly as well.
@@ -130,6 +133,10 @@ void prefill_kernel(const PrefillParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
   }
+  // Retire the Q loads here: otherwise the compiler's wait-count tracking
+  // keeps treating qf as in flight inside the tile loop and makes every
+  // S^T MFMA wait for the K/V prefetch issued just before it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched
 
   int hi = kv_len;
   if (CAUSAL) hi = min(kv_len, (mb + 1) * kBM + shift);
@@ -143,6 +150,20 @@ void prefill_kernel(const PrefillParams p) {
   float m_run = -INFINITY;  // scaled (log2) units
   float l_run = 0.f;
 
+  // K/V prefetch through buffer loads: the sequence's first row (this KV
+  // head) is the scalar base; each lane keeps a 32-bit byte offset, so the
+  // per-tile address is one clamp and one 24-bit multiply-add (no 64-bit
+  // vector arithmetic).  Rows past kv_len are clamped to the last row; their
+  // scores are masked to -inf.
+  const uint8_t* kseq = p.k + 2 * ((int64_t)k_start * p.k_st + (int64_t)kvh * p.k_sh);
+  const uint8_t* vseq = p.v + 2 * ((int64_t)k_start * p.v_st + (int64_t)kvh * p.v_sh);
+  // Record sizes end at the last row's final byte; loads past them read 0.
+  const int k_rec = (int)min((int64_t)max(kv_len - 1, 0) * p.k_st * 2 + 2 * D, (int64_t)0x7fffffff);
+  const int v_rec = (int)min((int64_t)max(kv_len - 1, 0) * p.v_st * 2 + 2 * D, (int64_t)0x7fffffff);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kseq, (short)0, k_rec, kBufFlags);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vseq, (short)0, v_rec, kBufFlags);
+  const int kst2 = 2 * (int)p.k_st;
+  const int vst2 = 2 * (int)p.v_st;
   u32x4 kreg[LOADS], vreg[LOADS];
   auto gload = [&](int tile) {
     const int n0 = tile * kBN;
@@ -151,9 +172,11 @@ void prefill_kernel(const PrefillParams p) {
       const int cid = tid + 256 * u;
       const int key = cid / CPR;
       const int col = cid % CPR;
-      const int kk = k_start + min(n0 + key, kv_len - 1);
-      kreg[u] = *reinterpret_cast<const u32x4*>(p.k + 2 * ((int64_t)kk * p.k_st + (int64_t)kvh * p.k_sh + 8 * col));
-      vreg[u] = *reinterpret_cast<const u32x4*>(p.v + 2 * ((int64_t)kk * p.v_st + (int64_t)kvh * p.v_sh + 8 * col));
+      const int row = min(n0 + key, kv_len - 1);
+      kreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              krs, (int)__umul24(row, kst2) + 16 * col, 0, 0));
+      vreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              vrs, (int)__umul24(row, vst2) + 16 * col, 0, 0));
     }
   };
   auto lstore = [&](int buf) {
@@ -208,19 +231,26 @@ void prefill_kernel(const PrefillParams p) {
     // ---- online softmax for query my_row (lane pair li, li + 32) ----
     const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
     float mx = -INFINITY;
+    if (!POS) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[jb][r] *= c;
+    }
+    if (need_mask) {  // wave-uniform: only tiles crossing kv_len or the diagonal
+      const int lim = CAUSAL ? min(kv_len - 1, my_row + shift) : kv_len - 1;
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
+          s[jb][r] = key <= lim ? s[jb][r] : -INFINITY;
+        }
+    }
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = POS ? s[jb][r] : s[jb][r] * c;
-        if (need_mask) {
-          const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
-          const bool ok = key < kv_len && (!CAUSAL || key <= my_row + shift);
-          x = ok ? x : -INFINITY;
-        }
-        s[jb][r] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
     mx = xor32<OpMax>(mx);
     if (POS) mx *= c;  // exact: rounding is monotonic and c > 0
     // Lazy rescale: keep m_run unless this tile's max exceeds it by kLazy.
@@ -375,6 +405,14 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   if ((align16 & 15) || (align8 & 7)) {
     fat_host::set_error("fat_prefill_varlen: q/k/v rows must be 16-byte aligned and out rows 8-byte aligned");
     return FAT_E_INVALID;
+  }
+  // Per-sequence K/V byte offsets are 32-bit (row * 2 * stride, 24-bit
+  // multiply): every kv_len is bounded by max_seqlen_k.
+  const int64_t kv_stride = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
+  if (kv_stride <= 0 || 2 * kv_stride >= (1 << 24) || (int64_t)a->max_seqlen_k * 2 * kv_stride >= 0x7fffffffLL) {
+    fat_host::set_error("fat_prefill_varlen: max_seqlen_k %d x token stride %lld exceeds the kernel's 32-bit "
+                        "per-sequence K/V offsets", a->max_seqlen_k, (long long)kv_stride);
+    return FAT_E_UNSUPPORTED;
   }
   if (a->max_seqlen_q == 0 || a->total_q == 0) return FAT_OK;  // nothing to compute
 
