@@ -8,19 +8,26 @@ flashattn_tile/autotune.py:76-106) / measured time, inputs resident in HBM.
 Two copies of the 537 MB pool alternate between steps so the 256 MB
 Infinity Cache cannot serve a step from the previous one.
 
-A step is one ``fat_paged_decode`` call through the C ABI (decode kernel,
-plus the log-sum-exp merge kernel when split_k > 1); HIP events on the
-launch stream bracket the K timed steps.  Split-K / waves-per-workgroup are
-chosen among a few candidates during warm-up (timed the same way) and
-reported in ``config``.  The prefill leg (causal varlen, seq 8192, 32/8
-heads, D128, fp16) is reported under ``prefill``.  ``cpu_baseline`` times the
-fp32 oracle (oracle/reference.py) on a bounded sample of the same workload.
+A step is one ``fat_paged_decode`` call through the C ABI (the decode
+kernel, plus the log-sum-exp merge kernel when split_k > 1); HIP events on
+the launch stream bracket the K timed steps.  split_k comes from the
+library's MI355X heuristic (``--tune`` times a few candidates instead).  The
+prefill leg (causal varlen, seq 8192, 32/8 heads, D128, fp16 and bf16) is
+reported under ``prefill`` with its own MFMA roofline.  ``cpu_baseline``
+times the fp32 oracle (oracle/reference.py) on a bounded sample of the
+headline workload on this host's cores.
+
+``--all-configs`` measures every BASELINE.json configuration (decode sweep,
+prefill lengths and mixed pack, int8/fp8 decode, long-context / skewed /
+MQA / D64 / page-size stress), each next to a CPU-oracle sample, and writes
+the table to ``--report`` (JSON) as well as stderr.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -28,7 +35,9 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"f16": 2516.6, "bf16": 2516.6}
+MFMA_PEAK_TFLOPS = 2516.6  # dense fp16 / bf16
+MALL_BYTES = 256 << 20
+FLUSH_BYTES = 512 << 20
 
 
 def _parse():
@@ -42,12 +51,34 @@ def _parse():
                     help="comma list of decode, prefill, cpu (the JSON line needs decode)")
     ap.add_argument("--tune", action="store_true",
                     help="time a few split_k / waves candidates in warm-up and keep the fastest")
-    ap.add_argument("--split-k", type=int, default=0, help="force split_k (0 = pick during warm-up)")
-    ap.add_argument("--waves", type=int, default=0, help="force waves per workgroup (0 = pick)")
+    ap.add_argument("--split-k", type=int, default=0, help="force split_k (0 = heuristic)")
+    ap.add_argument("--waves", type=int, default=0, help="force waves per workgroup (0 = library choice)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB copy kernel (torch.neg on fp32) three times, the known-size "
                          "reference that rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled by")
+    ap.add_argument("--all-configs", action="store_true", help="measure every BASELINE.json configuration")
+    ap.add_argument("--report", default="", help="with --all-configs: write the table to this JSON file")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle timing per sample")
     return ap.parse_args()
+
+
+def _cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))  # the GPU box's CPU share is 16 cores
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def copy_calibration(device, nbytes=1 << 30):
@@ -61,23 +92,49 @@ def copy_calibration(device, nbytes=1 << 30):
     return nbytes
 
 
-def _decode_inputs(batch, ctx, hq, hkv, d, page, dtype, seed, device, copies=2):
+# ---------------------------------------------------------------------------
+# Inputs and timing
+# ---------------------------------------------------------------------------
+def _paged_inputs(lens, hq, hkv, d, page, dtype, seed, device, copies=1, quant=None):
+    """Seeded paged decode inputs: q, [(k, v, k_scale, v_scale)] x copies, table, seq_lens
+    (device) and table, seq_lens (host).
+
+    Tables are a seeded permutation of the pool; with ``quant`` the pages are
+    drawn in fp32 and quantised per (page, KV head) by the product's
+    ``quantize_kv_pages`` (int8: absmax/127, fp8: absmax/448)."""
+    from flashattntile_amd.quant import quantize_kv_pages
+
     g = torch.Generator(device="cpu").manual_seed(seed)
-    pages_per = (ctx + page - 1) // page
-    num_pages = batch * pages_per
-    table = torch.randperm(num_pages, generator=g).to(torch.int32).view(batch, pages_per).to(device)
-    lens = torch.full((batch,), ctx, dtype=torch.int32, device=device)
-    q = torch.randn(batch, hq, d, generator=g).to(dtype).to(device)
+    pages_per = [max(1, math.ceil(n / page)) for n in lens]
+    maxp = max(pages_per)
+    num_pages = sum(pages_per)
+    perm = torch.randperm(num_pages, generator=g).to(torch.int32)
+    table = torch.zeros(len(lens), maxp, dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(pages_per):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    q = torch.randn(len(lens), hq, d, generator=g).to(dtype).to(device)
     gd = torch.Generator(device=device).manual_seed(seed + 1)
     pools = []
     for _ in range(copies):
-        k = torch.randn((num_pages, page, hkv, d), generator=gd, device=device, dtype=torch.float32).to(dtype)
-        v = torch.randn((num_pages, page, hkv, d), generator=gd, device=device, dtype=torch.float32).to(dtype)
-        pools.append((k, v))
-    return q, pools, table, lens
+        shape = (num_pages, page, hkv, d)
+        if quant is None:
+            k = torch.randn(shape, generator=gd, device=device, dtype=torch.float32).to(dtype)
+            v = torch.randn(shape, generator=gd, device=device, dtype=torch.float32).to(dtype)
+            pools.append((k, v, None, None))
+        else:
+            kf = torch.randn(shape, generator=gd, device=device, dtype=torch.float32)
+            vf = torch.randn(shape, generator=gd, device=device, dtype=torch.float32)
+            qk, qv, sk, sv, _ = quantize_kv_pages(kf, vf, quant)
+            del kf, vf
+            pools.append((qk, qv, sk, sv))
+    seq = torch.tensor(lens, dtype=torch.int32)
+    return q, pools, table.to(device), seq.to(device), table, seq
 
 
 def _time_steps(fn, steps, warmup, stream):
+    """Back-to-back steps bracketed by two HIP events on ``stream``; ms/step."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -88,16 +145,49 @@ def _time_steps(fn, steps, warmup, stream):
         fn(i)
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per step
+    return start.elapsed_time(end) / steps
 
 
+def _time_steps_flushed(fn, steps, warmup, stream, flush):
+    """Each step timed by its own event pair after a 512 MB write that evicts
+    the Infinity Cache (for working sets the MALL could otherwise hold)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    evs = []
+    for i in range(steps):
+        flush.fill_(i & 0xFF)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn(i)
+        e1.record(stream)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / steps
+
+
+def _time_cpu(fn, budget_s, max_reps=21):
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return min(times), len(times)
+
+
+# ---------------------------------------------------------------------------
+# Headline legs
+# ---------------------------------------------------------------------------
 def bench_decode(args, device):
     from flashattntile_amd import _hip
     from flashattntile_amd.autotune import bytes_decode_paged, decode_split_k
 
     B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
-    dtype = torch.float16
-    q, pools, table, lens = _decode_inputs(B, CTX, HQ, HKV, D, P, dtype, seed=1, device=device)
+    q, pools, table, lens, _, _ = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device=device,
+                                                copies=2)
     out = torch.empty_like(q)
     nbytes = bytes_decode_paged([CTX] * B, HQ, HKV, D)
     scale = D ** -0.5
@@ -107,7 +197,7 @@ def bench_decode(args, device):
 
     def make(split, waves):
         def step(i):
-            k, v = pools[i % len(pools)]
+            k, v, _, _ = pools[i % len(pools)]
             _hip.paged_decode(q, k, v, table, lens, out, P, scale, split, workspace=ws, stream=handle,
                               waves_per_group=waves)
         return step
@@ -124,43 +214,61 @@ def bench_decode(args, device):
     torch.cuda.synchronize()
     ms = _time_steps(make(s, w), args.steps, args.warmup, stream)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    del pools
     return {
         "ms": ms,
         "gbs": gbs,
         "bytes": nbytes,
         "split_k": s,
-        "waves_per_group": w,
+        "waves_per_group": w or (8 if B * HKV * s < 512 else 4),
         "tuning_ms": {f"sk{a}_w{b}": round(t, 5) for (a, b), t in tuning.items()},
         "shape": {"batch": B, "ctx": CTX, "num_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "page_size": P},
     }
 
 
-def bench_prefill(args, device, seq=8192):
-    from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import flops_attention
+def _prefill_case(lens, hq, hkv, d, dtype, seed, device):
+    g = torch.Generator(device=device).manual_seed(seed)
+    total = sum(lens)
+    q = torch.randn(total, hq, d, generator=g, device=device).to(dtype)
+    k = torch.randn(total, hkv, d, generator=g, device=device).to(dtype)
+    v = torch.randn(total, hkv, d, generator=g, device=device).to(dtype)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32, device=device)
+    return q, k, v, cu
 
-    HQ, HKV, D = 32, 8, 128
-    dtype = torch.float16
-    g = torch.Generator(device=device).manual_seed(7)
-    q = torch.randn(seq, HQ, D, generator=g, device=device).to(dtype)
-    k = torch.randn(seq, HKV, D, generator=g, device=device).to(dtype)
-    v = torch.randn(seq, HKV, D, generator=g, device=device).to(dtype)
-    cu = torch.tensor([0, seq], dtype=torch.int32, device=device)
+
+def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7):
+    from flashattntile_amd import _hip
+    from flashattntile_amd.autotune import flops_attention_varlen
+
+    q, k, v, cu = _prefill_case(lens, hq, hkv, d, dtype, seed, device)
     out = torch.empty_like(q)
-    ws_bytes = _hip.prefill_workspace_bytes(seq, HKV, D)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
+    mx = max(lens)
 
     def step(i):
-        _hip.prefill_varlen(q, k, v, cu, cu, out, seq, seq, True, D ** -0.5, workspace=ws, stream=handle)
+        _hip.prefill_varlen(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, stream=handle)
 
-    steps = max(5, args.steps // 10)
-    ms = _time_steps(step, steps, max(3, args.warmup // 4), stream)
-    flops = flops_attention(HQ, D, seq, seq, causal=True)
+    ms = _time_steps(step, steps, warmup, stream)
+    flops = flops_attention_varlen(hq, d, lens, lens, causal=True)
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flops": flops, "seq": seq, "steps": steps,
-            "mfma_peak_tflops": MFMA_PEAK_TFLOPS["f16"], "frac": tflops / MFMA_PEAK_TFLOPS["f16"]}
+    return {"ms": ms, "tflops": tflops, "flops": flops, "frac": tflops / MFMA_PEAK_TFLOPS}
+
+
+def bench_prefill(args, device, seq=8192):
+    res = {}
+    steps = max(10, args.steps // 10)
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        r = run_prefill([seq], dt, device, steps, max(3, args.warmup // 4))
+        res[name] = {
+            "ms": round(r["ms"], 4),
+            "tflops": round(r["tflops"], 1),
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"]},
+        }
+    res["workload"] = f"prefill_causal_seq{seq}_h32_kv8_d128"
+    res["steps"] = steps
+    return res
 
 
 def cpu_baseline_decode(budget_s=12.0):
@@ -170,40 +278,148 @@ def cpu_baseline_decode(budget_s=12.0):
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    cores = min(cores, 16)
+    cores = _cores()
     torch.set_num_threads(cores)
     B, CTX, HQ, HKV, D, P = 4, 4096, 32, 8, 128, 16
-    q, pools, table, lens = _decode_inputs(B, CTX, HQ, HKV, D, P, torch.float16, seed=1, device="cpu", copies=1)
-    k, v = pools[0]
-    for _ in range(2):
-        ref_attention_paged(q, k, v, table, lens)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        ref_attention_paged(q, k, v, table, lens)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 21:
-            break
+    q, pools, _, _, table, lens = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device="cpu")
+    k, v, _, _ = pools[0]
+    best, reps = _time_cpu(lambda: ref_attention_paged(q, k, v, table, lens), budget_s)
     nbytes = bytes_decode_paged([CTX] * B, HQ, HKV, D)
-    best = min(times)
     return {
         "value": nbytes / best / 1e9,
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
         "sample": f"fp32 oracle ref_attention_paged on 4 of the 32 sequences (ctx 4096, 32/8 heads, D128, "
-                  f"page 16, fp16 pages upcast); min of {len(times)} runs after 2 warm-ups",
+                  f"page 16, fp16 pages upcast); min of {reps} runs after 1 warm-up; {_cpu_model()}",
         "ms": best * 1e3,
     }
 
 
+# ---------------------------------------------------------------------------
+# Every BASELINE.json configuration
+# ---------------------------------------------------------------------------
+def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, quant=None, cpu_seqs=2):
+    from flashattntile_amd import _hip
+    from flashattntile_amd.autotune import bytes_decode_paged, decode_split_k
+    from oracle.reference import ref_attention_paged
+
+    kv_elem = 1 if quant else 2
+    pool_bytes = sum(lens) * hkv * d * 2 * kv_elem
+    copies = 1 if pool_bytes >= 2 * MALL_BYTES else 2
+    q, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, torch.float16, seed=11,
+                                                             device=device, copies=copies, quant=quant)
+    maxp = table.shape[1]
+    sk = split or decode_split_k(len(lens), hq, hkv, maxp)
+    out = torch.empty_like(q)
+    ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens), hq, d, sk)), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+    handle = int(stream.cuda_stream)
+
+    def step(i):
+        k, v, ks, vs = pools[i % copies]
+        _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
+                          k_scale=ks, v_scale=vs)
+
+    steps = max(20, args.steps // 4)
+    if pool_bytes * copies < 2 * MALL_BYTES:
+        ms = _time_steps_flushed(step, steps, 5, stream, flush)
+        timing = "per-launch events after a 512 MB cache flush"
+    else:
+        ms = _time_steps(step, steps, 5, stream)
+        timing = f"back-to-back, {copies} pool copies alternating"
+    nbytes = bytes_decode_paged(lens, hq, hkv, d, kv_elem_bytes=kv_elem, page_size=page, quantized=bool(quant))
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # CPU oracle on the first `cpu_seqs` sequences (dequantised to fp16 first for 8-bit caches)
+    nb = min(cpu_seqs, len(lens))
+    k0, v0, ks0, vs0 = pools[0]
+    used = table_cpu[:nb].flatten().unique().long()
+    kc, vc = k0[used.to(device)].cpu(), v0[used.to(device)].cpu()
+    remap = torch.full((k0.shape[0],), -1, dtype=torch.int64)
+    remap[used] = torch.arange(used.numel())
+    tab = remap[table_cpu[:nb].long()].clamp_min(0).to(torch.int32)
+    if quant:
+        from oracle.quant_ref import dequantize_pages
+        kc = dequantize_pages(kc, ks0[used.to(device)].cpu(), torch.float16)
+        vc = dequantize_pages(vc, vs0[used.to(device)].cpu(), torch.float16)
+    qc = q[:nb].cpu()
+    best, reps = _time_cpu(lambda: ref_attention_paged(qc, kc, vc, tab, seq_cpu[:nb]), args.cpu_budget / 4)
+    cpu_bytes = bytes_decode_paged(lens[:nb], hq, hkv, d, kv_elem_bytes=kv_elem, page_size=page,
+                                   quantized=bool(quant))
+    del pools
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "decode", "value": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "timing": timing,
+            "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
+                    "sample": f"{nb} of {len(lens)} sequences, min of {reps}"}}
+
+
+def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
+    from flashattntile_amd.autotune import flops_attention_varlen
+    from oracle.reference import ref_attention_varlen
+
+    r = run_prefill(lens, dtype, device, max(10, args.steps // 10), 3, hq=hq, hkv=hkv, d=d)
+    # CPU oracle: the query heads of one KV head over the first sequence
+    group = hq // hkv
+    L = lens[0]
+    g = torch.Generator().manual_seed(3)
+    qc = torch.randn(L, group, d, generator=g).to(dtype)
+    kc = torch.randn(L, 1, d, generator=g).to(dtype)
+    vc = torch.randn(L, 1, d, generator=g).to(dtype)
+    cu = torch.tensor([0, L], dtype=torch.int32)
+    best, reps = _time_cpu(lambda: ref_attention_varlen(qc, kc, vc, cu, cu, causal=True), args.cpu_budget / 4,
+                           max_reps=5)
+    cpu_flops = flops_attention_varlen(group, d, [L], [L], causal=True)
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "prefill", "value": round(r["tflops"], 1), "unit": "TFLOP/s",
+            "frac": round(r["frac"], 4), "us": round(r["ms"] * 1e3, 2), "flops": r["flops"],
+            "cpu": {"value": round(cpu_flops / best / 1e12, 5), "unit": "TFLOP/s",
+                    "sample": f"{group} query heads / 1 KV head of sequence 0 (L={L}), min of {reps}"}}
+
+
+def all_configs(args, device):
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=device)
+    rows = []
+
+    def emit(row):
+        rows.append(row)
+        print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
+              f"{row['us']:9.1f} us)  cpu {row['cpu']['value']} {row['cpu']['unit']}", file=sys.stderr, flush=True)
+
+    # fp16 decode sweep (and bf16 at the headline shape)
+    for B in (1, 8, 32, 128):
+        for ctx in (128, 1024, 4096, 16384):
+            emit(_decode_row(f"decode fp16 B{B} ctx{ctx}", [ctx] * B, 32, 8, 128, 16, device, args, flush))
+    emit(_decode_row("decode bf16 B32 ctx4096", [4096] * 32, 32, 8, 128, 16, device, args, flush))
+    # prefill fp16 / bf16, L in 512..8192 and the mixed pack
+    g = torch.Generator().manual_seed(2024)
+    mixed = torch.randint(1, 4097, (8,), generator=g).tolist()
+    mixed[0] |= 1
+    for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        for L in (512, 1024, 2048, 4096, 8192):
+            emit(_prefill_row(f"prefill {dn} causal L{L}", [L], dt, device, args))
+        emit(_prefill_row(f"prefill {dn} causal mixed8 {sum(mixed)} tok", mixed, dt, device, args))
+    # quantised decode B128 ctx16384
+    for mode, mn in (("int8", "int8"), ("float8_e4m3fn", "fp8")):
+        emit(_decode_row(f"decode {mn} B128 ctx16384", [16384] * 128, 32, 8, 128, 16, device, args, flush,
+                         quant=mode, cpu_seqs=1))
+    # stress
+    emit(_decode_row("decode fp16 B1 ctx131072 split16", [131072], 32, 8, 128, 16, device, args, flush, split=16,
+                     cpu_seqs=1))
+    g = torch.Generator().manual_seed(64)
+    skew = [int(math.exp(x)) for x in (torch.rand(64, generator=g) * (math.log(65536) - math.log(16))
+                                       + math.log(16)).tolist()]
+    emit(_decode_row(f"decode fp16 skewed64 sum{sum(skew)}", skew, 32, 8, 128, 16, device, args, flush))
+    emit(_decode_row("decode fp16 MQA 32/1 B32 ctx4096", [4096] * 32, 32, 1, 128, 16, device, args, flush))
+    emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
+    for page in (32, 64):
+        emit(_decode_row(f"decode fp16 P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device, args, flush))
+    return rows
+
+
 def _traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs, if committed."""
+    """HBM bytes per launch measured by rocprofv3 PMC runs (profiles/traffic.json)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as fh:
@@ -229,6 +445,16 @@ def main():
     if not _hip.is_loaded():
         print(f"bench.py: HIP library unavailable: {_hip.load_error()}", file=sys.stderr)
         sys.exit(2)
+    torch.set_num_threads(_cores())
+
+    if args.all_configs:
+        rows = all_configs(args, device)
+        report = {"cores": _cores(), "cpu_model": _cpu_model(), "rows": rows,
+                  "device": torch.cuda.get_device_name(device)}
+        if args.report:
+            with open(args.report, "w") as fh:
+                json.dump(report, fh, indent=1)
+        return
 
     if args.copy_calibration:
         n = copy_calibration(device)
@@ -246,15 +472,12 @@ def main():
               f"waves={dec['waves_per_group']})", file=sys.stderr, flush=True)
     pre = None
     if "prefill" in legs:
-        try:
-            pre = bench_prefill(args, device)
-            print(f"# prefill seq8192: {pre['tflops']:.1f} TFLOP/s ({pre['ms']:.3f} ms)", file=sys.stderr,
-                  flush=True)
-        except RuntimeError as exc:  # prefill kernel not available in this build
-            pre = {"error": str(exc)}
+        pre = bench_prefill(args, device)
+        print(f"# prefill seq8192: fp16 {pre['f16']['tflops']:.1f} TFLOP/s ({pre['f16']['ms']:.3f} ms), "
+              f"bf16 {pre['bf16']['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     cpu = None
     if "cpu" in legs:
-        cpu = cpu_baseline_decode()
+        cpu = cpu_baseline_decode(args.cpu_budget)
         print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} cores", file=sys.stderr, flush=True)
     if dec is None:
         return
@@ -291,8 +514,9 @@ def main():
         },
         "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "ms"},
         "prefill": pre,
-        "decode_tuning_ms": dec["tuning_ms"],
     }
+    if dec["tuning_ms"]:
+        line["decode_tuning_ms"] = dec["tuning_ms"]
     print(json.dumps(line), flush=True)
 
 
