@@ -28,6 +28,11 @@
 //   * the 1-D grid walks query blocks longest-first (causal balance) and
 //     assigns the query heads that share a KV head to the same XCD
 //     (workgroup id mod 8), so K/V blocks are reused from that XCD's L2.
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
+
 #include "fat_common.h"
 
 namespace fat {
@@ -78,6 +83,10 @@ constexpr int kBufFlags = 0x00020000;
 // exceeds it by more than this many log2 units; p = 2^(x - m) then stays
 // below 2^kLazy, which fp16/bf16 P and the fp32 sums hold exactly as well.
 constexpr float kLazy = 8.0f;
+#ifndef FAT_PF_PP_MIN
+#define FAT_PF_PP_MIN 512
+#endif
+constexpr u32 kOnesF16x2 = 0x3C003C00u;  // (1.0, 1.0) as packed fp16
 
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
@@ -151,10 +160,8 @@ void prefill_kernel(const PrefillParams p) {
   float l_run = 0.f;
 
   // K/V prefetch through buffer loads: the sequence's first row (this KV
-  // head) is the scalar base; each lane keeps a 32-bit byte offset, so the
-  // per-tile address is one clamp and one 24-bit multiply-add (no 64-bit
-  // vector arithmetic).  Rows past kv_len are clamped to the last row; their
-  // scores are masked to -inf.
+  // head) is the scalar base and each lane keeps a 32-bit byte offset, so a
+  // tile's addresses cost one add per load (no 64-bit vector arithmetic).
   const uint8_t* kseq = p.k + 2 * ((int64_t)k_start * p.k_st + (int64_t)kvh * p.k_sh);
   const uint8_t* vseq = p.v + 2 * ((int64_t)k_start * p.v_st + (int64_t)kvh * p.v_sh);
   // Record sizes end at the last row's final byte; loads past them read 0.
@@ -164,30 +171,58 @@ void prefill_kernel(const PrefillParams p) {
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vseq, (short)0, v_rec, kBufFlags);
   const int kst2 = 2 * (int)p.k_st;
   const int vst2 = 2 * (int)p.v_st;
+  // Per-lane byte offset of this lane's first chunk; load u adds
+  // u * (256 / CPR) rows.  Rows at or past kv_len fall outside the buffer
+  // record and read as zero (their scores are masked), so no clamp is needed.
+  const int koff0 = (int)__umul24(tid / CPR, kst2) + 16 * (tid % CPR);
+  const int voff0 = (int)__umul24(tid / CPR, vst2) + 16 * (tid % CPR);
+  constexpr int kRowsPerLoad = 256 / CPR;
   u32x4 kreg[LOADS], vreg[LOADS];
-  auto gload = [&](int tile) {
-    const int n0 = tile * kBN;
+  auto gload_k = [&](int tile) {
+    const int base = koff0 + tile * kBN * kst2;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+      kreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              krs, base + u * kRowsPerLoad * kst2, 0, 0));
+  };
+  auto gload_v = [&](int tile) {
+    const int base = voff0 + tile * kBN * vst2;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+      vreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              vrs, base + u * kRowsPerLoad * vst2, 0, 0));
+  };
+  auto lstore_k = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
-      const int key = cid / CPR;
-      const int col = cid % CPR;
-      const int row = min(n0 + key, kv_len - 1);
-      kreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              krs, (int)__umul24(row, kst2) + 16 * col, 0, 0));
-      vreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              vrs, (int)__umul24(row, vst2) + 16 * col, 0, 0));
+      *reinterpret_cast<u32x4*>(&Ks[buf][(cid / CPR) * K_RS + 8 * (cid % CPR)]) = kreg[u];
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore_v = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
-      const int key = cid / CPR;
-      const int col = cid % CPR;
-      *reinterpret_cast<u32x4*>(&Ks[buf][key * K_RS + 8 * col]) = kreg[u];
-      *reinterpret_cast<u32x4*>(&Vs[buf][key * V_RS + 8 * col]) = vreg[u];
+      *reinterpret_cast<u32x4*>(&Vs[buf][(cid / CPR) * V_RS + 8 * (cid % CPR)]) = vreg[u];
     }
+  };
+
+  // S^T = K Q^T for the two 32-key blocks of the K tile in Ks[buf].
+  auto qk = [&](int buf, f32x16* s) {
+    const uint16_t* Kb = Ks[buf];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
+    // The two 32-key blocks are independent accumulator chains; alternating
+    // them keeps dependent MFMAs apart.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Kb[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
+        s[jb] = Mfma<T>::mma(a, qf[ks], s[jb]);
+      }
   };
 
   // Lane roles of the transposed V reads (see lds_read_tr16).
@@ -197,46 +232,54 @@ void prefill_kernel(const PrefillParams p) {
   const int tr_row = 4 * (tr_G >> 1) + tr_c;      // + 32 jb + 16 t (+ 8)
   const int tr_col = 16 * (tr_G & 1) + 4 * tr_j;  // + 32 db
 
+  // Software pipeline (one workgroup barrier per tile).  Iteration t
+  // computes S(t+1) on the MFMA pipe while the VALU runs the softmax of
+  // S(t), then O += V(t) P(t).  K therefore lives two tiles ahead in LDS and
+  // V one tile ahead: iteration t stores K(t+2) into Ks[t%2] and V(t+1) into
+  // Vs[(t+1)%2] (both buffers were last read in iteration t-1) and issues
+  // the global loads of K(t+3) and V(t+2).
+  f32x16 s_cur[2];
   if (n_tiles > 0) {
-    gload(0);
-    lstore(0);
-    if (n_tiles > 1) gload(1);
-  }
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int buf = tile & 1;
-    // Tile `tile` is in Ks/Vs[buf]; every wave is done with tile - 1, whose
-    // buffer now takes tile + 1 (already in registers).
+    gload_k(0);
+    gload_v(0);
+    lstore_k(0);
+    lstore_v(0);
+    if (n_tiles > 1) {
+      gload_k(1);
+      lstore_k(1);
+      gload_v(1);
+    }
+    if (n_tiles > 2) gload_k(2);
     __syncthreads();
-    if (tile + 1 < n_tiles) {
-      lstore(buf ^ 1);
-      if (tile + 2 < n_tiles) gload(tile + 2);
+    qk(0, s_cur);
+  }
+  // One pipeline step.  HAS_NEXT (compile time) is false only for the last
+  // tile, so S(t+1), the exponentials and the PV MFMAs of every other tile
+  // sit in one basic block that the scheduler can interleave; the rare lazy
+  // rescale runs in a branch before that block.
+  auto step = [&](int tile, auto has_next_tag) {
+    constexpr bool HAS_NEXT = decltype(has_next_tag)::value;
+    const int buf = tile & 1;
+    __syncthreads();
+    if (tile + 2 < n_tiles) {
+      lstore_k(buf);
+      if (tile + 3 < n_tiles) gload_k(tile + 3);
+    }
+    if (HAS_NEXT) {
+      lstore_v(buf ^ 1);
+      if (tile + 2 < n_tiles) gload_v(tile + 2);
     }
     const int n0 = tile * kBN;
-    const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
 
-    // ---- S^T = K Q^T for two 32-key blocks ----
-    f32x16 s[2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&Kb[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
-        s[jb] = Mfma<T>::mma(a, qf[ks], s[jb]);
-      }
-    }
-
-    // ---- online softmax for query my_row (lane pair li, li + 32) ----
-    const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
-    float mx = -INFINITY;
+    // ---- scores of tile t: scale (c <= 0 only), mask, row max ----
     if (!POS) {
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[jb][r] *= c;
+        for (int r = 0; r < 16; ++r) s_cur[jb][r] *= c;
     }
+    const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
     if (need_mask) {  // wave-uniform: only tiles crossing kv_len or the diagonal
       const int lim = CAUSAL ? min(kv_len - 1, my_row + shift) : kv_len - 1;
 #pragma unroll
@@ -244,41 +287,37 @@ void prefill_kernel(const PrefillParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
-          s[jb][r] = key <= lim ? s[jb][r] : -INFINITY;
+          s_cur[jb][r] = key <= lim ? s_cur[jb][r] : -INFINITY;
         }
     }
+    float mx = -INFINITY;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[jb][r]);
     mx = xor32<OpMax>(mx);
     if (POS) mx *= c;  // exact: rounding is monotonic and c > 0
-    // Lazy rescale: keep m_run unless this tile's max exceeds it by kLazy.
-    float alpha = 1.f;
-    if (mx > m_run + kLazy) {
-      alpha = fast_exp2(m_run - mx);
-      m_run = mx;
-    }
-    const float cm = POS ? c : 1.f;
-    const float nm = -m_run;
-    float ls = 0.f;
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(__builtin_fmaf(s[jb][r], cm, nm));
-        s[jb][r] = e;
-        ls += e;
-      }
-    l_run = __builtin_fmaf(l_run, alpha, ls);
-    if (__any(alpha != 1.f)) {
+    // Lazy rescale: m_run moves only when this tile's max exceeds it by kLazy.
+    const bool grow = mx > m_run + kLazy;
+    if (__any(grow)) {
+      const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+      m_run = grow ? mx : m_run;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
     }
 
-    // ---- P^T operands (k-step t of key block jb uses accumulator regs 8t..8t+7) ----
+    // ---- S(t+1) on the MFMA pipe, interleaved with P(t) = 2^(s c - m) ----
+#ifdef FAT_PF_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+    f32x16 s_nxt[2];
+    if constexpr (HAS_NEXT) qk(buf ^ 1, s_nxt);
+    const float cm = POS ? c : 1.f;
+    const float nm = -m_run;
+    float ls = 0.f;
     u32x4 pf[2][2];
     u32x4 pl[2][2];
 #pragma unroll
@@ -287,14 +326,20 @@ void prefill_kernel(const PrefillParams p) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-          const float x0 = s[jb][8 * t + 2 * e2];
-          const float x1 = s[jb][8 * t + 2 * e2 + 1];
+          const float x0 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2], cm, nm));
+          const float x1 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2 + 1], cm, nm));
+          // P^T operand: k-step t of key block jb uses accumulator regs 8t..8t+7.
           const u32 hp = Pair<T>::pack(x0, x1);
           pf[jb][t][e2] = hp;
           if constexpr (SPLIT_P) {
             pl[jb][t][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+            ls += x0 + x1;
+          } else {
+            // l sums the fp16-rounded weights the PV MFMA uses (one dot2 per pair).
+            ls = Pair<T>::dot2(hp, kOnesF16x2, ls);
           }
         }
+    l_run += ls;
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -312,9 +357,287 @@ void prefill_kernel(const PrefillParams p) {
           if constexpr (SPLIT_P) acc[db] = Mfma<T>::mma(a, pl[jb][t], acc[db]);
         }
       }
-  }
+#ifdef FAT_PF_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+    if constexpr (HAS_NEXT) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) s_cur[jb] = s_nxt[jb];
+    }
+  };
+  for (int tile = 0; tile + 1 < n_tiles; ++tile) step(tile, std::true_type{});
+  if (n_tiles > 0) step(n_tiles - 1, std::false_type{});
 
   // ---- epilogue: O = O^T / l, lane writes 4 consecutive dims per store ----
+  const float l_tot = xor32<OpAdd>(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (my_row < q_len) {
+    uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * db + 4 * g + 8 * rr;
+        u32x2 pk;
+        pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
+        pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + 2 * d0) = pk;
+      }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Ping-pong variant for grids that fill the chip: 8 waves = 2 groups of 4,
+// 256 query rows per workgroup (32 per wave).  Waves w and w + 4 share a
+// SIMD and run opposite phases, separated by one workgroup barrier per
+// half-step ("slot"):
+//   MFMA phase of step t:  S(t+1) = K(t+1) Q^T  and  O += V(t) P(t)
+//   VALU phase of step t:  softmax of S(t) -> P(t) (mask, max, lazy rescale,
+//                          exponentials), plus this group's staging duty
+// Group A (waves 0-3) runs MFMA(t) in slot 2t+2 and VALU(t) in slot 2t+1;
+// group B (waves 4-7) one slot later.  So while one wave of a SIMD keeps the
+// matrix core busy, the other does its softmax.  Group A stages K tiles
+// (stores K(t+1) into Ks[(t+1)&1] in slot 2t+1), group B stages V tiles
+// (stores V(t) into Vs[t&1] in slot 2t); each buffer's previous tile was
+// last read two slots earlier and the new one is first read one slot later.
+// ---------------------------------------------------------------------------
+constexpr int kPBM = 256;
+
+template <typename T, int D, bool CAUSAL, bool POS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_pp_kernel(const PrefillParams p) {
+  constexpr int KS = D / 16;
+  constexpr int DB = D / 32;
+  constexpr int K_RS = D + 8;
+  constexpr int V_RS = D + 32;
+  constexpr int CPR = D / 8;
+  constexpr int LOADS = kBN * CPR / 256;  // one 256-thread group stages a whole tile
+  constexpr int kRowsPerLoad = 256 / CPR;
+  constexpr bool SPLIT_P = std::is_same<T, BF16>::value;
+  static_assert(LOADS >= 1, "tile too small");
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * V_RS];
+
+  const int per = p.B * p.H;
+  const int outer = blockIdx.x / per;
+  const int rem = blockIdx.x - outer * per;
+  const int b = rem / p.H;
+  const int j = rem - b * p.H;
+  const int kvh = j % p.Hkv;
+  const int h = kvh * p.group + j / p.Hkv;
+  const int mb = p.nqb - 1 - outer;
+
+  const int q_start = p.cu_q[b];
+  const int q_len = p.cu_q[b + 1] - q_start;
+  const int k_start = p.cu_k[b];
+  const int kv_len = p.cu_k[b + 1] - k_start;
+  if (mb * kPBM >= q_len) return;  // uniform over the workgroup
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = w >> 2;     // 0: group A (stages K), 1: group B (stages V)
+  const int gt = tid & 255;   // thread index inside the group
+  const int g = lane >> 5;
+  const int li = lane & 31;
+  const int shift = kv_len - q_len;
+  const int row0 = mb * kPBM + w * 32;
+  const int my_row = row0 + li;
+  const float c = p.scale_log2;
+
+  u32x4 qf[KS];
+  {
+    const int qr = min(my_row, q_len - 1);
+    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): retire the Q loads before the loop
+
+  int hi = kv_len;
+  if (CAUSAL) hi = min(kv_len, (mb + 1) * kPBM + shift);
+  const int n_tiles = hi > 0 ? (hi + kBN - 1) / kBN : 0;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // Staging: group A streams K tiles, group B V tiles, through buffer loads
+  // (scalar per-sequence base; rows past kv_len read as zero).
+  const int st = grp ? (int)p.v_st : (int)p.k_st;
+  const int st2 = 2 * st;
+  const int64_t sh = grp ? p.v_sh : p.k_sh;
+  const uint8_t* seq = (grp ? p.v : p.k) + 2 * ((int64_t)k_start * st + (int64_t)kvh * sh);
+  const int rec = (int)min((int64_t)max(kv_len - 1, 0) * st2 + 2 * D, (int64_t)0x7fffffff);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)seq, (short)0, rec, kBufFlags);
+  const int off0 = (int)__umul24(gt / CPR, st2) + 16 * (gt % CPR);
+  const int lds_rs = grp ? V_RS : K_RS;
+  uint16_t* const lds0 = grp ? &Vs[0][0] : &Ks[0][0];
+  const int lds_buf = grp ? kBN * V_RS : kBN * K_RS;
+  const int lds_off = (gt / CPR) * lds_rs + 8 * (gt % CPR);
+  u32x4 stage[LOADS];
+  auto gload = [&](int tile) {
+    const int base = off0 + tile * kBN * st2;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+      stage[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs, base + u * kRowsPerLoad * st2, 0, 0));
+  };
+  auto lstore = [&](int buf) {
+    uint16_t* dst = lds0 + buf * lds_buf + lds_off;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+      *reinterpret_cast<u32x4*>(dst + u * kRowsPerLoad * lds_rs) = stage[u];
+  };
+
+  const int tr_c = (lane & 15) >> 2;
+  const int tr_j = lane & 3;
+  const int tr_G = lane >> 4;
+  const int tr_row = 4 * (tr_G >> 1) + tr_c;
+  const int tr_col = 16 * (tr_G & 1) + 4 * tr_j;
+
+  f32x16 s[2];
+  u32x4 pf[2][2];
+  u32x4 pl[2][2];
+
+  // S(t) = K(t) Q^T into s.
+  auto qk = [&](int t) {
+    const uint16_t* Kb = Ks[t & 1];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[jb][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&Kb[(jb * 32 + li) * K_RS + 16 * ks + 8 * g]);
+        s[jb] = Mfma<T>::mma(a, qf[ks], s[jb]);
+      }
+  };
+  // O += V(t) P(t).
+  auto pv = [&](int t) {
+    const uint16_t* Vb = Vs[t & 1];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int vrow = jb * 32 + 16 * tt + tr_row;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const uint16_t* vp = &Vb[vrow * V_RS + 32 * db + tr_col];
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
+          const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
+          acc[db] = Mfma<T>::mma(a, pf[jb][tt], acc[db]);
+          if constexpr (SPLIT_P) acc[db] = Mfma<T>::mma(a, pl[jb][tt], acc[db]);
+        }
+      }
+  };
+  // Staging duty of step t (group A: K(t+1), group B: V(t+1)), then fetch t+2.
+  auto stage_step = [&](int t) {
+    if (t + 1 < n_tiles) {
+      lstore((t + 1) & 1);
+      if (t + 2 < n_tiles) gload(t + 2);
+    }
+  };
+  // Softmax of S(t) -> P(t) (mask, max, lazy rescale, exponentials).
+  auto softmax = [&](int t) {
+    const int n0 = t * kBN;
+    if (!POS) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[jb][r] *= c;
+    }
+    const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
+    if (need_mask) {
+      const int lim = CAUSAL ? min(kv_len - 1, my_row + shift) : kv_len - 1;
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = n0 + jb * 32 + (r & 3) + 4 * g + 8 * (r >> 2);
+          s[jb][r] = key <= lim ? s[jb][r] : -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
+    mx = xor32<OpMax>(mx);
+    if (POS) mx *= c;
+    const bool grow = mx > m_run + kLazy;
+    if (__any(grow)) {
+      const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+      m_run = grow ? mx : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+    }
+    const float cm = POS ? c : 1.f;
+    const float nm = -m_run;
+    float ls = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float x0 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2], cm, nm));
+          const float x1 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2 + 1], cm, nm));
+          const u32 hp = Pair<T>::pack(x0, x1);
+          pf[jb][tt][e2] = hp;
+          if constexpr (SPLIT_P) {
+            pl[jb][tt][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+            ls += x0 + x1;
+          } else {
+            ls = Pair<T>::dot2(hp, kOnesF16x2, ls);
+          }
+        }
+    l_run += ls;
+  };
+
+  // Prologue: K(0) to LDS (group A); K(1) (A) / V(0) (B) into registers.
+  // Every wave then passes 2 * n_tiles + 2 barriers; group B runs one slot
+  // behind group A, so the two waves of each SIMD are in opposite phases.
+  if (n_tiles > 0) {
+    gload(0);
+    if (grp == 0) {
+      lstore(0);
+      if (n_tiles > 1) gload(1);
+    }
+    if (grp == 1) {
+      __syncthreads();
+      stage_step(-1);  // V(0) -> Vs[0], fetch V(1)
+    }
+    __syncthreads();
+    qk(0);
+    __syncthreads();
+    stage_step(0);
+    softmax(0);
+    for (int t = 1; t < n_tiles; ++t) {
+      __syncthreads();
+      qk(t);
+      pv(t - 1);
+      __syncthreads();
+      stage_step(t);
+      softmax(t);
+    }
+    __syncthreads();
+    pv(n_tiles - 1);
+    if (grp == 0) __syncthreads();
+  }
+
   const float l_tot = xor32<OpAdd>(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (my_row < q_len) {
@@ -348,9 +671,23 @@ void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStr
   }
 }
 
+template <typename T, int D, bool CAUSAL>
+void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
+  if (pos) {
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true>), grid, dim3(512), 0, stream, prm);
+  } else {
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false>), grid, dim3(512), 0, stream, prm);
+  }
+}
+
 template <typename T, int D>
-int launch_prefill_t(const fat::PrefillParams& prm, bool causal, dim3 grid, hipStream_t stream) {
+int launch_prefill_t(const fat::PrefillParams& prm, bool causal, bool pingpong, dim3 grid, hipStream_t stream) {
   const bool pos = prm.scale_log2 > 0.f;
+  if (pingpong) {
+    if (causal) launch_prefill_pp_c<T, D, true>(prm, pos, grid, stream);
+    else launch_prefill_pp_c<T, D, false>(prm, pos, grid, stream);
+    return fat_host::launch_status("prefill_pp_kernel");
+  }
   if (causal) launch_prefill_c<T, D, true>(prm, pos, grid, stream);
   else launch_prefill_c<T, D, false>(prm, pos, grid, stream);
   return fat_host::launch_status("prefill_kernel");
@@ -435,7 +772,19 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = a->num_heads / a->num_kv_heads;
-  prm.nqb = (a->max_seqlen_q + fat::kBM - 1) / fat::kBM;
+  // The 8-wave ping-pong kernel needs a grid of at least FAT_PF_PP_MIN
+  // 256-row workgroups to fill the chip; smaller problems use the 4-wave,
+  // 128-row kernel (twice the workgroups).
+  const int64_t nqb_pp = (a->max_seqlen_q + fat::kPBM - 1) / fat::kPBM;
+  bool pingpong = nqb_pp * a->batch * a->num_heads >= FAT_PF_PP_MIN;
+  // FAT_PREFILL_KERNEL=pingpong|4wave overrides the choice (tests exercise
+  // both kernels on every shape); anything else keeps the automatic one.
+  if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
+    if (!strcmp(force, "pingpong")) pingpong = true;
+    else if (!strcmp(force, "4wave")) pingpong = false;
+  }
+  const int bm = pingpong ? fat::kPBM : fat::kBM;
+  prm.nqb = (a->max_seqlen_q + bm - 1) / bm;
   prm.scale_log2 = a->softmax_scale * fat::kLog2e;
   const int64_t n = (int64_t)prm.nqb * a->batch * a->num_heads;
   if (n > 0x7fffffff) {
@@ -446,9 +795,9 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const bool causal = a->causal != 0;
   if (a->dtype == FAT_DTYPE_F16) {
-    return D == 128 ? launch_prefill_t<fat::F16, 128>(prm, causal, grid, stream)
-                    : launch_prefill_t<fat::F16, 64>(prm, causal, grid, stream);
+    return D == 128 ? launch_prefill_t<fat::F16, 128>(prm, causal, pingpong, grid, stream)
+                    : launch_prefill_t<fat::F16, 64>(prm, causal, pingpong, grid, stream);
   }
-  return D == 128 ? launch_prefill_t<fat::BF16, 128>(prm, causal, grid, stream)
-                  : launch_prefill_t<fat::BF16, 64>(prm, causal, grid, stream);
+  return D == 128 ? launch_prefill_t<fat::BF16, 128>(prm, causal, pingpong, grid, stream)
+                  : launch_prefill_t<fat::BF16, 64>(prm, causal, pingpong, grid, stream);
 }

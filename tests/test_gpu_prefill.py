@@ -22,6 +22,14 @@ DEV = "cuda"
 ODD_LENS = [1, 17, 255, 1000]
 
 
+@pytest.fixture(params=["auto", "pingpong", "4wave"])
+def kernel(request, monkeypatch):
+    """Run the test with the library's automatic choice and with each of the
+    two prefill kernels forced (8-wave ping-pong, 4-wave), whatever the shape."""
+    monkeypatch.setenv("FAT_PREFILL_KERNEL", request.param)
+    return request.param
+
+
 def _ref32(q, k, v, cu_q, cu_k, causal, scale=None):
     return ref_attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu_q.cpu(), cu_k.cpu(), causal=causal,
                                 softmax_scale=scale, return_fp32=True)
@@ -31,8 +39,8 @@ def _ref32(q, k, v, cu_q, cu_k, causal, scale=None):
 @pytest.mark.parametrize("h,hk", [(8, 8), (8, 2), (8, 1), (32, 8)])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_prefill_matches_oracle(dtype, d, h, hk, causal):
-    label = f"prefill {dtype} D{d} H{h}/{hk} causal={causal}"
+def test_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
+    label = f"prefill {kernel} {dtype} D{d} H{h}/{hk} causal={causal}"
     print(label, flush=True)
     q, k, v, cu = make_varlen(ODD_LENS, h, hk, d, dtype, seed=d + h + hk, device=DEV)
     out = prefill_attention(q, k, v, cu, cu, max(ODD_LENS), max(ODD_LENS), causal=causal)
@@ -43,10 +51,10 @@ def test_prefill_matches_oracle(dtype, d, h, hk, causal):
 
 @pytest.mark.parametrize("seqlen", [1, 2, 63, 64, 65, 127, 128, 129, 1000])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_prefill_single_odd_length(seqlen, dtype):
+def test_prefill_single_odd_length(seqlen, dtype, kernel):
     q, k, v, cu = make_varlen([seqlen], 8, 2, 128, dtype, seed=8, device=DEV)
     for causal in (True, False):
-        label = f"prefill single L{seqlen} {dtype} causal={causal}"
+        label = f"prefill {kernel} single L{seqlen} {dtype} causal={causal}"
         print(label, flush=True)
         out = prefill_attention(q, k, v, cu, cu, seqlen, seqlen, causal=causal)
         torch.cuda.synchronize()
@@ -55,9 +63,9 @@ def test_prefill_single_odd_length(seqlen, dtype):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_prefill_kv_longer_than_q(dtype, causal):
+def test_prefill_kv_longer_than_q(dtype, causal, kernel):
     """Bottom-right causal alignment with kv_len > q_len (chunked-prefill shape)."""
-    label = f"prefill q<kv {dtype} causal={causal}"
+    label = f"prefill {kernel} q<kv {dtype} causal={causal}"
     print(label, flush=True)
     g = torch.Generator().manual_seed(3)
     lq, lk = [3, 50, 129, 1], [10, 300, 129, 77]
@@ -72,12 +80,12 @@ def test_prefill_kv_longer_than_q(dtype, causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_prefill_mixed_pack_baseline(dtype):
+def test_prefill_mixed_pack_baseline(dtype, kernel):
     """BASELINE configs[2] mixed pack: 8 sequences, lengths uniform in [1, 4096]."""
     g = torch.Generator().manual_seed(2024)
     lens = torch.randint(1, 4097, (8,), generator=g).tolist()
     lens[0] |= 1  # at least one odd length
-    label = f"prefill mixed {lens} {dtype}"
+    label = f"prefill {kernel} mixed {lens} {dtype}"
     print(label, flush=True)
     q, k, v, cu = make_varlen(lens, 32, 8, 128, dtype, seed=5, device=DEV)
     out = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True)
@@ -87,12 +95,12 @@ def test_prefill_mixed_pack_baseline(dtype):
 
 @pytest.mark.parametrize("seqlen", [512, 2048, 8192])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_prefill_long_sequence_head_subsets(seqlen, dtype):
+def test_prefill_long_sequence_head_subsets(seqlen, dtype, kernel):
     """BASELINE configs[2] single sequences (32/8 heads, D128, causal): all
     heads are computed by the kernel; the oracle checks the query heads of
     KV heads 0 and 7 (the oracle's [H, L, L] fp32 scores are kept small)."""
     q, k, v, cu = make_varlen([seqlen], 32, 8, 128, dtype, seed=seqlen, device=DEV)
-    label = f"prefill L{seqlen} {dtype}"
+    label = f"prefill {kernel} L{seqlen} {dtype}"
     print(label, flush=True)
     out = prefill_attention(q, k, v, cu, cu, seqlen, seqlen, causal=True)
     torch.cuda.synchronize()
