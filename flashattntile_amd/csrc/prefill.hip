@@ -86,7 +86,6 @@ constexpr float kLazy = 8.0f;
 #ifndef FAT_PF_PP_MIN
 #define FAT_PF_PP_MIN 512
 #endif
-constexpr u32 kOnesF16x2 = 0x3C003C00u;  // (1.0, 1.0) as packed fp16
 
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
@@ -331,13 +330,8 @@ void prefill_kernel(const PrefillParams p) {
           // P^T operand: k-step t of key block jb uses accumulator regs 8t..8t+7.
           const u32 hp = Pair<T>::pack(x0, x1);
           pf[jb][t][e2] = hp;
-          if constexpr (SPLIT_P) {
-            pl[jb][t][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
-            ls += x0 + x1;
-          } else {
-            // l sums the fp16-rounded weights the PV MFMA uses (one dot2 per pair).
-            ls = Pair<T>::dot2(hp, kOnesF16x2, ls);
-          }
+          if constexpr (SPLIT_P) pl[jb][t][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+          ls += x0 + x1;  // fp32 adds: v_dot2 would stall the other wave's MFMAs
         }
     l_run += ls;
 
@@ -403,6 +397,10 @@ void prefill_kernel(const PrefillParams p) {
 // last read two slots earlier and the new one is first read one slot later.
 // ---------------------------------------------------------------------------
 constexpr int kPBM = 256;
+// Lazy-rescale bound of the ping-pong kernel (log2 units) and the partial
+// row-sum level above which its exact softmax path runs.
+constexpr float kLazyPP = 15.0f;
+constexpr float kLazyPPSum = 32768.0f;  // 2^kLazyPP
 
 template <typename T, int D, bool CAUSAL, bool POS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -567,43 +565,58 @@ void prefill_pp_kernel(const PrefillParams p) {
           s[jb][r] = key <= lim ? s[jb][r] : -INFINITY;
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
-    mx = xor32<OpMax>(mx);
-    if (POS) mx *= c;
-    const bool grow = mx > m_run + kLazy;
-    if (__any(grow)) {
-      const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
-      m_run = grow ? mx : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-    }
+    // P(t) = 2^(s c - m_run) against the running max, without a row max:
+    // the exact path (row max, lazy rescale, recompute) runs only on the
+    // first tile or when some lane's partial row sum exceeds 2^kLazyPP --
+    // which every p > 2^kLazyPP forces.  P and the fp32 sums hold values up
+    // to 2^kLazyPP exactly as well as values up to 1.
     const float cm = POS ? c : 1.f;
-    const float nm = -m_run;
-    float ls = 0.f;
+    auto compute_p = [&]() -> float {
+      const float nm = -m_run;
+      float lsq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // four partial row sums
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+      for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const float x0 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2], cm, nm));
-          const float x1 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2 + 1], cm, nm));
-          const u32 hp = Pair<T>::pack(x0, x1);
-          pf[jb][tt][e2] = hp;
-          if constexpr (SPLIT_P) {
-            pl[jb][tt][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
-            ls += x0 + x1;
-          } else {
-            ls = Pair<T>::dot2(hp, kOnesF16x2, ls);
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const float x0 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2], cm, nm));
+            const float x1 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2 + 1], cm, nm));
+            const u32 hp = Pair<T>::pack(x0, x1);
+            pf[jb][tt][e2] = hp;
+            if constexpr (SPLIT_P) pl[jb][tt][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+            // fp32 adds, not v_dot2: a dot2 on one wave stalls the other
+            // wave's MFMAs (measured on gfx950), undoing the ping-pong overlap.
+            lsq[jb][tt] += x0 + x1;
           }
-        }
+      return (lsq[0][0] + lsq[0][1]) + (lsq[1][0] + lsq[1][1]);
+    };
+    float ls = 0.f;
+    bool exact = t == 0;
+    if (!exact) {
+      ls = compute_p();
+      exact = __any(!(ls <= kLazyPPSum));  // also catches inf / NaN sums
+    }
+    if (exact) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
+      mx = xor32<OpMax>(mx);
+      if (POS) mx *= c;
+      const bool grow = mx > m_run + kLazyPP;
+      if (__any(grow)) {
+        const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+        m_run = grow ? mx : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+      }
+      ls = compute_p();
+    }
     l_run += ls;
   };
 
@@ -626,10 +639,19 @@ void prefill_pp_kernel(const PrefillParams p) {
     stage_step(0);
     softmax(0);
     for (int t = 1; t < n_tiles; ++t) {
+      // sched_barrier keeps every instruction inside its phase (the compiler
+      // would otherwise move MFMAs across the workgroup barrier); the MFMA
+      // phase runs at raised priority so its wave wins issue contention.
+      __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(2);
       qk(t);
       pv(t - 1);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
       stage_step(t);
       softmax(t);
     }
