@@ -397,6 +397,31 @@ void prefill_kernel(const PrefillParams p) {
 // last read two slots earlier and the new one is first read one slot later.
 // ---------------------------------------------------------------------------
 constexpr int kPBM = 256;
+
+// Scheduling groups of one MFMA phase of NE operand entries: the first NS
+// entries (S^T blocks) take one LDS read each and feed one MFMA; the rest
+// (PV blocks) take two transposed reads each and feed MPP MFMAs.  The reads of
+// entry e + LOOK are issued right after the MFMA(s) of entry e.
+template <int E, int LOOK, int NE, int NS>
+struct MfmaPhaseReads {
+  static __device__ __forceinline__ void apply() {
+    if constexpr (E < LOOK && E < NE) {
+      __builtin_amdgcn_sched_group_barrier(0x100, E < NS ? 1 : 2, 0);
+      MfmaPhaseReads<E + 1, LOOK, NE, NS>::apply();
+    }
+  }
+};
+template <int E, int NE, int NS, int MPP, int LOOK>
+struct MfmaPhaseOrder {
+  static __device__ __forceinline__ void apply() {
+    if constexpr (E == 0) MfmaPhaseReads<0, LOOK, NE, NS>::apply();
+    if constexpr (E < NE) {
+      __builtin_amdgcn_sched_group_barrier(0x008, E < NS ? 1 : MPP, 0);
+      if constexpr (E + LOOK < NE) __builtin_amdgcn_sched_group_barrier(0x100, (E + LOOK) < NS ? 1 : 2, 0);
+      MfmaPhaseOrder<E + 1, NE, NS, MPP, LOOK>::apply();
+    }
+  }
+};
 // Lazy-rescale bound of the ping-pong kernel (log2 units) and the partial
 // row-sum level above which its exact softmax path runs.
 constexpr float kLazyPP = 15.0f;
@@ -638,16 +663,22 @@ void prefill_pp_kernel(const PrefillParams p) {
     __syncthreads();
     stage_step(0);
     softmax(0);
-    for (int t = 1; t < n_tiles; ++t) {
+    // Causal: tiles past this wave's last visible key are fully masked for
+    // it; from tile nv on the wave only stages tiles and keeps the barrier
+    // count (two per tile) of the rest of the workgroup.
+    const int nv = CAUSAL ? min(n_tiles, (row0 + 31 + shift) / kBN + 1) : n_tiles;
+    for (int t = 1; t < nv; ++t) {
       // sched_barrier keeps every instruction inside its phase (the compiler
       // would otherwise move MFMAs across the workgroup barrier); the MFMA
-      // phase runs at raised priority so its wave wins issue contention.
+      // phase runs at raised priority so its wave wins issue contention, and
+      // its LDS operand reads run 4 MFMAs ahead of their use.
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(2);
       qk(t);
       pv(t - 1);
+      MfmaPhaseOrder<0, 2 * KS + 4 * DB, 2 * KS, SPLIT_P ? 2 : 1, 4>::apply();
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
@@ -656,7 +687,12 @@ void prefill_pp_kernel(const PrefillParams p) {
       softmax(t);
     }
     __syncthreads();
-    pv(n_tiles - 1);
+    pv(nv - 1);
+    for (int t = nv; t < n_tiles; ++t) {
+      __syncthreads();
+      stage_step(t);
+      __syncthreads();
+    }
     if (grp == 0) __syncthreads();
   }
 
