@@ -59,6 +59,7 @@ def _parse():
     ap.add_argument("--all-configs", action="store_true", help="measure every BASELINE.json configuration")
     ap.add_argument("--report", default="", help="with --all-configs: write the table to this JSON file")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle timing per sample")
+    ap.add_argument("--only", default="", help="with --all-configs: run only rows whose name contains this text")
     return ap.parse_args()
 
 
@@ -149,14 +150,17 @@ def _time_steps(fn, steps, warmup, stream):
 
 
 def _time_steps_flushed(fn, steps, warmup, stream, flush):
-    """Each step timed by its own event pair after a 512 MB write that evicts
-    the Infinity Cache (for working sets the MALL could otherwise hold)."""
+    """Each step timed by its own event pair after a 512 MB read that evicts
+    the Infinity Cache (for working sets the MALL could otherwise hold).  The
+    flush only reads (a max-reduction into 8 bytes), so it leaves no dirty
+    lines for the timed kernel to write back."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     evs = []
+    sink = torch.empty((), dtype=flush.dtype, device=flush.device)
     for i in range(steps):
-        flush.fill_(i & 0xFF)
+        torch.amax(flush, dim=0, out=sink)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
@@ -183,7 +187,7 @@ def _time_cpu(fn, budget_s, max_reps=21):
 # ---------------------------------------------------------------------------
 def bench_decode(args, device):
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged, decode_split_k
+    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
 
     B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
     q, pools, table, lens, _, _ = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device=device,
@@ -195,17 +199,22 @@ def bench_decode(args, device):
     handle = int(stream.cuda_stream)
     ws = torch.empty(_hip.decode_workspace_bytes(B, HQ, D, 64), dtype=torch.uint8, device=device)
 
+    pages = (CTX + P - 1) // P
+    auto_split, auto_chunk = decode_partition(B, HQ, HKV, pages, B * pages)
+
     def make(split, waves):
+        pps = auto_chunk if split == auto_split else 0
+
         def step(i):
             k, v, _, _ = pools[i % len(pools)]
             _hip.paged_decode(q, k, v, table, lens, out, P, scale, split, workspace=ws, stream=handle,
-                              waves_per_group=waves)
+                              waves_per_group=waves, pages_per_split=pps)
         return step
 
     if args.tune:
         cands = [(s, w) for s in (1, 2, 3, 4, 8) for w in (4, 8)]
     else:
-        cands = [(args.split_k or decode_split_k(B, HQ, HKV, (CTX + P - 1) // P), args.waves or 0)]
+        cands = [(args.split_k or auto_split, args.waves or 0)]
     tuning = {}
     if len(cands) > 1:
         for cand in cands:
@@ -300,8 +309,10 @@ def cpu_baseline_decode(budget_s=12.0):
 # Every BASELINE.json configuration
 # ---------------------------------------------------------------------------
 def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, quant=None, cpu_seqs=2):
+    if args.only and args.only not in name:
+        return None
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged, decode_split_k
+    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
     from oracle.reference import ref_attention_paged
 
     kv_elem = 1 if quant else 2
@@ -310,7 +321,11 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     q, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, torch.float16, seed=11,
                                                              device=device, copies=copies, quant=quant)
     maxp = table.shape[1]
-    sk = split or decode_split_k(len(lens), hq, hkv, maxp)
+    total_pages = sum(math.ceil(n / page) for n in lens)
+    if split:
+        sk, pps = split, 0
+    else:
+        sk, pps = decode_partition(len(lens), hq, hkv, maxp, total_pages)
     out = torch.empty_like(q)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens), hq, d, sk)), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
@@ -319,7 +334,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     def step(i):
         k, v, ks, vs = pools[i % copies]
         _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
-                          k_scale=ks, v_scale=vs)
+                          k_scale=ks, v_scale=vs, pages_per_split=pps)
 
     steps = max(20, args.steps // 4)
     if pool_bytes * copies < 2 * MALL_BYTES:
@@ -350,12 +365,15 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     torch.cuda.empty_cache()
     return {"config": name, "kind": "decode", "value": round(gbs, 1), "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "pages_per_split": pps,
             "timing": timing,
             "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
                     "sample": f"{nb} of {len(lens)} sequences, min of {reps}"}}
 
 
 def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
+    if args.only and args.only not in name:
+        return None
     from flashattntile_amd.autotune import flops_attention_varlen
     from oracle.reference import ref_attention_varlen
 
@@ -379,10 +397,12 @@ def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
 
 
 def all_configs(args, device):
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=device)
+    flush = torch.ones(FLUSH_BYTES // 8, dtype=torch.float64, device=device)
     rows = []
 
     def emit(row):
+        if row is None:
+            return
         rows.append(row)
         print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
               f"{row['us']:9.1f} us)  cpu {row['cpu']['value']} {row['cpu']['unit']}", file=sys.stderr, flush=True)

@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum fat_dtype
 DT_F16 = 0
@@ -79,6 +79,7 @@ class DecodeArgs(ctypes.Structure):
         ("waves_per_group", _c_i32),
         ("q_dtype", _c_i32),
         ("kv_dtype", _c_i32),
+        ("pages_per_split", _c_i32),
         ("softmax_scale", ctypes.c_float),
     ]
 
@@ -225,6 +226,7 @@ def paged_decode(
     v_scale: torch.Tensor | None = None,
     stream: int | None = None,
     waves_per_group: int = 0,
+    pages_per_split: int = 0,
 ) -> None:
     """Enqueue ``fat_paged_decode`` for already-validated device tensors."""
     a = DecodeArgs()
@@ -255,6 +257,7 @@ def paged_decode(
     a.waves_per_group = int(waves_per_group)
     a.q_dtype = dtype_code(q.dtype)
     a.kv_dtype = dtype_code(k_cache.dtype)
+    a.pages_per_split = int(pages_per_split)
     a.softmax_scale = float(softmax_scale)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")

@@ -27,6 +27,7 @@ __all__ = [
     "bytes_decode_paged",
     "arithmetic_intensity",
     "decode_split_k",
+    "decode_partition",
     "MI355X_CUS",
 ]
 
@@ -122,3 +123,34 @@ def decode_split_k(batch: int, num_heads: int, num_kv_heads: int, max_pages: int
     split = math.ceil(num_cus / base)
     split = min(split, max_split, max(1, max_pages // min_pages_per_split))
     return int(max(1, split))
+
+
+def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: int, total_pages: int,
+                     num_cus: int = MI355X_CUS, min_pages_per_split: int = 8,
+                     max_split: int = 16) -> tuple[int, int]:
+    """``(split_k, pages_per_split)`` for a possibly ragged batch on MI355X.
+
+    Every partition holds the same number of pages and split_k covers the
+    longest sequence.  A uniform batch (``batch * max_pages`` below twice
+    ``total_pages``) is spread over about one workgroup per CU with at most
+    ``max_split`` partitions -- the same launch as :func:`decode_split_k`.  A
+    skewed batch gets many small partitions (about 16 workgroups per CU, up to
+    64 partitions), so the long sequences are streamed by many workgroups and
+    the dispatcher balances the uneven rest.  Both regimes were measured on
+    MI355X (32/8 heads, D128, page 16: the B x ctx sweep and 64 log-uniform
+    lengths in [16, 65536]).
+    """
+    group = max(1, num_heads // max(1, num_kv_heads))
+    heads_per_wg = 8 if group >= 8 else 4
+    groups = num_kv_heads * math.ceil(group / heads_per_wg)
+    max_pages = max(1, int(max_pages))
+    total_pages = max(1, int(total_pages))
+    skewed = batch * max_pages >= 2 * total_pages
+    target_wgs = 16 * num_cus if skewed else num_cus
+    cap = 64 if skewed else max_split
+    chunk = max(min_pages_per_split, math.ceil(total_pages * groups / target_wgs))
+    split = math.ceil(max_pages / chunk)
+    if split > cap:
+        split = cap
+        chunk = math.ceil(max_pages / split)
+    return int(max(1, split)), int(chunk)

@@ -50,6 +50,7 @@ struct DecodeParams {
   int64_t o_sb, o_sh;
   int32_t H, Hkv, group, hg_per_kv;
   int32_t P, log2P, num_pages, max_pages;
+  int32_t pps_fixed;  // pages per partition, 0 = ceil(np / split_k)
   float scale_log2;  // softmax_scale * log2(e)
 };
 
@@ -132,9 +133,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   int seq_len = p.lens[b];
   seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
   const int np = (seq_len + p.P - 1) >> p.log2P;
-  const int pps = (np + S - 1) / S;
+  const int pps = p.pps_fixed > 0 ? p.pps_fixed : (np + S - 1) / S;
   const int pb = split * pps;
-  const int pe = min(np, pb + pps);
+  const int pe = split == S - 1 ? np : min(np, pb + pps);
   const int t_begin = pb << p.log2P;
   const int t_end = min(seq_len, pe << p.log2P);
   const int n_units = t_end > t_begin ? (t_end - t_begin + 15) >> 4 : 0;
@@ -529,6 +530,10 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     fat_host::set_error("fat_paged_decode: waves_per_group must be 0 (auto), 4 or 8, got %d", a->waves_per_group);
     return FAT_E_INVALID;
   }
+  if (a->pages_per_split < 0) {
+    fat_host::set_error("fat_paged_decode: pages_per_split must be >= 0, got %d", a->pages_per_split);
+    return FAT_E_INVALID;
+  }
   if (a->split_k > 1 && !a->workspace) {
     fat_host::set_error("fat_paged_decode: split_k > 1 needs a workspace");
     return FAT_E_INVALID;
@@ -582,6 +587,7 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   prm.log2P = log2P;
   prm.num_pages = a->num_pages;
   prm.max_pages = a->max_pages;
+  prm.pps_fixed = a->pages_per_split;
   prm.scale_log2 = a->softmax_scale * fat::kLog2e;
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);

@@ -27,7 +27,7 @@ from __future__ import annotations
 import torch
 
 from .. import _hip
-from ..autotune import decode_split_k
+from ..autotune import decode_partition
 from ..paging import PagedKVCache, _check_layout, cache_stats
 
 __all__ = [
@@ -37,17 +37,21 @@ __all__ = [
     "paged_decode_launch",
 ]
 
-# split_k None -> MI355X heuristic; num_warps is the number of 64-lane waves
-# per workgroup (4 or 8; None lets the library choose from the grid size);
-# num_stages is accepted for signature compatibility with the reference's
-# Triton knob and validated the same way, but the HIP kernel's pipeline depth
-# is fixed (one 16-token unit prefetched per wave).
-DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2}
+# split_k None -> MI355X partition heuristic (split_k and pages_per_split from
+# the batch's lengths); an explicit split_k keeps the reference's partitioning
+# (ceil(pages / split_k) per sequence) unless pages_per_split is also given.
+# num_warps is the number of 64-lane waves per workgroup (4 or 8; None lets the
+# library choose from the grid size); num_stages is accepted for signature
+# compatibility with the reference's Triton knob and validated the same way,
+# but the HIP kernel's pipeline depth is fixed (one 16-token unit prefetched
+# per wave).
+DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2, "pages_per_split": None}
 
 _QUANT_DTYPES = tuple(d for d in (torch.int8, getattr(torch, "float8_e4m3fn", None)) if d is not None)
 
 
-def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache) -> dict:
+def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, max_len: int,
+                    total_pages: int) -> dict:
     resolved = dict(DEFAULT_CONFIG)
     if config is not None:
         unknown = set(config) - set(DEFAULT_CONFIG)
@@ -55,13 +59,22 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache) -
             raise ValueError(f"unknown decode config keys: {sorted(unknown)}")
         resolved.update(config)
     if resolved["split_k"] is None:
-        resolved["split_k"] = decode_split_k(int(q.shape[0]), int(q.shape[1]), cache.num_kv_heads,
-                                             cache.max_pages_per_seq)
+        max_pages = -(-max_len // cache.page_size)
+        split, chunk = decode_partition(int(q.shape[0]), int(q.shape[1]), cache.num_kv_heads, max_pages,
+                                        total_pages)
+        resolved["split_k"] = split
+        if resolved["pages_per_split"] is None:
+            resolved["pages_per_split"] = chunk
+    if resolved["pages_per_split"] is None:
+        resolved["pages_per_split"] = 0
     split_k = resolved["split_k"]
     if not isinstance(split_k, int) or isinstance(split_k, bool) or split_k < 1:
         raise ValueError(f"split_k must be a positive integer, got {split_k}")
     if split_k > 64:
         raise ValueError(f"split_k must be <= 64, got {split_k}")
+    pps = resolved["pages_per_split"]
+    if not isinstance(pps, int) or isinstance(pps, bool) or pps < 0:
+        raise ValueError(f"pages_per_split must be a non-negative integer, got {pps}")
     if resolved["num_warps"] not in (None, 1, 2, 4, 8, 16, 32):
         raise ValueError(f"num_warps must be a power of two <= 32, got {resolved['num_warps']}")
     if resolved["num_warps"] not in (None, 4, 8):
@@ -71,8 +84,10 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache) -
     return resolved
 
 
-def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
-    """``decode.py:503-522`` + ``paging.validate_cache``, with one sync."""
+def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> tuple[int, int]:
+    """``decode.py:503-522`` + ``paging.validate_cache``, with one sync.
+
+    Returns ``(max_len, total_pages)`` for the partition heuristic."""
     if not isinstance(cache, PagedKVCache):
         raise TypeError("cache must be a PagedKVCache")
     _check_layout(cache)
@@ -88,7 +103,7 @@ def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
         raise ValueError("q and cache must live on the same device")
     if not q.is_floating_point():
         raise ValueError(f"q must be floating point, got {q.dtype}")
-    min_len, max_len, lo, hi = cache_stats(cache)
+    min_len, max_len, lo, hi, total_pages = cache_stats(cache, with_total_pages=True)
     if min_len < 0:
         raise AssertionError("seq_lens must be non-negative")
     capacity = cache.capacity
@@ -101,6 +116,7 @@ def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> None:
             raise AssertionError(f"page_table references page {hi} but cache has {cache.num_pages} pages")
     if min_len <= 0:
         raise ValueError("decode requires every sequence to hold at least one cached token")
+    return max_len, total_pages
 
 
 def _require_rocm(q: torch.Tensor, cache: PagedKVCache, what: str) -> None:
@@ -121,6 +137,7 @@ def paged_decode_launch(
     workspace: torch.Tensor | None = None,
     scales=None,
     waves_per_group: int | None = None,
+    pages_per_split: int = 0,
 ) -> torch.Tensor:
     """Enqueue the HIP decode without validation or synchronisation.
 
@@ -141,7 +158,8 @@ def paged_decode_launch(
         v_scale = scales["v"] if isinstance(scales, dict) else scales.v
     _hip.paged_decode(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, out,
                       cache.page_size, softmax_scale, split_k, workspace=workspace,
-                      k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0)
+                      k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0,
+                      pages_per_split=pages_per_split)
     return out
 
 
@@ -163,15 +181,16 @@ def paged_decode_attention(
     ``q.dtype``.
     """
     del grouped  # every launch is grouped on MI355X
-    _validate_decode_inputs(q, cache)
+    max_len, total_pages = _validate_decode_inputs(q, cache)
     scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
-    cfg = _resolve_config(config, q, cache)
+    cfg = _resolve_config(config, q, cache, max_len, total_pages)
     _require_rocm(q, cache, "paged_decode_attention")
     if q.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"paged_decode_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
     if cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
-    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"])
+    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"],
+                               pages_per_split=cfg["pages_per_split"])
 
 
 def paged_decode_attention_fp8(
@@ -187,7 +206,7 @@ def paged_decode_attention_fp8(
     with ``"k"``/``"v"``), fp32 ``[num_pages, num_kv_heads]``.  Pages are
     dequantised in registers as ``(float(x) * scale).to(q.dtype)``.
     """
-    _validate_decode_inputs(q, cache)
+    max_len, total_pages = _validate_decode_inputs(q, cache)
     k_scale = scales["k"] if isinstance(scales, dict) else scales.k
     v_scale = scales["v"] if isinstance(scales, dict) else scales.v
     quant_dtype = cache.k_cache.dtype
@@ -197,7 +216,7 @@ def paged_decode_attention_fp8(
     if tuple(k_scale.shape) != expected or tuple(v_scale.shape) != expected:
         raise ValueError(f"scales must have shape {expected}, got {tuple(k_scale.shape)}")
     scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
-    cfg = _resolve_config(config, q, cache)
+    cfg = _resolve_config(config, q, cache, max_len, total_pages)
     _require_rocm(q, cache, "paged_decode_attention_fp8")
     if not (k_scale.is_cuda and v_scale.is_cuda):
         raise RuntimeError("paged_decode_attention_fp8: scales must be ROCm device tensors")
@@ -207,4 +226,4 @@ def paged_decode_attention_fp8(
         raise ValueError("scales must be float32")
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"],
                                scales={"k": k_scale.contiguous(), "v": v_scale.contiguous()},
-                               waves_per_group=cfg["num_warps"])
+                               waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"])

@@ -97,17 +97,18 @@ def _check_layout(cache: PagedKVCache) -> None:
     _require(pt.device == sl.device, "page_table and seq_lens must live on the same device")
 
 
-def cache_stats(cache: PagedKVCache) -> tuple[int, int, int, int]:
+def cache_stats(cache: PagedKVCache, with_total_pages: bool = False) -> tuple[int, ...]:
     """``(min_len, max_len, min_page, max_page)`` in ONE device->host copy.
 
     The page range covers ``page_table[:, :ceil(max_len / page_size)]`` for every
     row, the same entries ``paging.py:123-129`` inspects.  With no cached token
-    the page range is reported as ``(0, -1)``.
+    the page range is reported as ``(0, -1)``.  ``with_total_pages`` appends
+    ``sum_b ceil(seq_lens[b] / page_size)`` (same copy).
     """
     sl = cache.seq_lens
     pt = cache.page_table
     if sl.numel() == 0:
-        return 0, 0, 0, -1
+        return (0, 0, 0, -1, 0) if with_total_pages else (0, 0, 0, -1)
     max_len = sl.max()
     need = torch.div(max_len + (cache.page_size - 1), cache.page_size, rounding_mode="floor")
     cols = torch.arange(pt.shape[1], device=pt.device)
@@ -120,12 +121,16 @@ def cache_stats(cache: PagedKVCache) -> tuple[int, int, int, int]:
     else:
         min_page = torch.tensor(big, dtype=torch.int32, device=pt.device)
         max_page = torch.tensor(small, dtype=torch.int32, device=pt.device)
-    stats = torch.stack([sl.min().to(torch.int64), max_len.to(torch.int64),
-                         min_page.to(torch.int64), max_page.to(torch.int64)]).cpu().tolist()
-    min_len, max_len_i, lo, hi = (int(x) for x in stats)
-    if lo == big:
-        lo, hi = 0, -1
-    return min_len, max_len_i, lo, hi
+    parts = [sl.min().to(torch.int64), max_len.to(torch.int64), min_page.to(torch.int64),
+             max_page.to(torch.int64)]
+    if with_total_pages:
+        pages = torch.div(sl.to(torch.int64).clamp_min(0) + (cache.page_size - 1), cache.page_size,
+                          rounding_mode="floor")
+        parts.append(pages.sum())
+    stats = [int(x) for x in torch.stack(parts).cpu().tolist()]
+    if stats[2] == big:
+        stats[2], stats[3] = 0, -1
+    return tuple(stats)
 
 
 def validate_cache(cache: PagedKVCache, *, check_pages: bool = True) -> tuple[int, int]:

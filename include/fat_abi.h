@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 1
+#define FAT_ABI_VERSION 2
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -66,9 +66,14 @@ enum fat_status {
  * Strides are in elements; the head_dim axis must be contiguous.
  *
  * Query head h reads KV head h / (num_heads / num_kv_heads).  The context of
- * sequence b is split into split_k partitions of ceil(ceil(len/P)/split_k)
- * pages each; with split_k > 1 the partitions are merged by a log-sum-exp
- * reduction through `workspace`, which must hold
+ * sequence b is split into split_k partitions.  With pages_per_split == 0 each
+ * holds ceil(ceil(len/P)/split_k) pages (the reference's split kernel,
+ * flashattn_tile/kernels/decode.py:271-276); with pages_per_split > 0 every
+ * partition holds that many pages, so work per workgroup is the same for
+ * short and long sequences of a ragged batch (partitions past a sequence's
+ * end are empty, and the last partition takes any pages beyond
+ * split_k * pages_per_split).  With split_k > 1 the partitions are merged by
+ * a log-sum-exp reduction through `workspace`, which must hold
  * fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k) bytes
  * (it may be NULL when split_k == 1).  int8/fp8 pages are dequantised as
  * round_to_q_dtype(float(x) * scale) before the fp32 attention, exactly as
@@ -102,6 +107,7 @@ typedef struct fat_decode_args {
   int32_t waves_per_group; /* 0 = chosen by the library, else 4 or 8 */
   int32_t q_dtype;  /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 (also the out dtype) */
   int32_t kv_dtype; /* q_dtype, FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3           */
+  int32_t pages_per_split; /* 0 = ceil(pages / split_k) per sequence        */
   float softmax_scale;
 } fat_decode_args;
 

@@ -53,3 +53,16 @@ def test_split_heuristic():
     assert at.decode_split_k(1, 32, 8, 8192) == 16  # capped
     assert at.decode_split_k(128, 32, 8, 1024) == 1
     assert at.decode_split_k(1, 32, 8, 3) == 1  # partitions of at least 8 pages
+
+
+def test_partition_heuristic():
+    # uniform batches: same launches as decode_split_k
+    assert at.decode_partition(32, 32, 8, 256, 32 * 256) == (1, 256)
+    assert at.decode_partition(8, 32, 8, 256, 8 * 256) == (4, 64)
+    assert at.decode_partition(1, 32, 8, 64, 64) == (8, 8)
+    # capped at 16 partitions, pages re-spread over them
+    assert at.decode_partition(1, 32, 8, 8192, 8192) == (16, 512)
+    # skewed batch: small partitions (~16 workgroups per CU), split covers the longest sequence
+    split, chunk = at.decode_partition(64, 32, 8, 4096, 40019)
+    assert chunk == -(-40019 * 8 // (16 * 256)) and split == -(-4096 // chunk)
+    assert split * chunk >= 4096 and split <= 64

@@ -188,3 +188,33 @@ def test_native_library_is_the_path():
     assert hip.is_loaded(), hip.load_error()
     with open("/proc/self/maps") as fh:
         assert "libfat_hip.so" in fh.read()
+
+
+@pytest.mark.parametrize("split_k,pps", [(4, 16), (2, 8), (8, 3), (1, 5), (3, 200)])
+def test_fixed_pages_per_split(split_k, pps):
+    """Fixed-size partitions (pages_per_split > 0): equal to the oracle whether
+    split_k * pages_per_split covers the longest sequence or falls short (then
+    the last partition takes the remaining pages)."""
+    label = f"decode fixed partitions sk{split_k} pps{pps}"
+    print(label, flush=True)
+    lens = [5, 1000, 37, 4096, 16, 2500]
+    q, cache = _case(lens, 32, 8, 128, 16, torch.float16, seed=50 + pps)
+    out = paged_decode_attention(q, cache, config={"split_k": split_k, "pages_per_split": pps})
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label=label)
+
+
+def test_auto_partition_skewed_batch():
+    """config=None on a skewed batch picks fixed-size partitions."""
+    from flashattntile_amd.kernels.decode import _resolve_config
+    print("decode auto partition skewed", flush=True)
+    g = torch.Generator().manual_seed(77)
+    lens = [int(math.exp(x)) for x in (torch.rand(48, generator=g) * (math.log(30000) - math.log(16))
+                                        + math.log(16)).tolist()]
+    q, cache = _case(lens, 32, 8, 128, 16, torch.bfloat16, seed=7)
+    total = sum(-(-n // 16) for n in lens)
+    cfg = _resolve_config(None, q, cache, max(lens), total)
+    assert cfg["pages_per_split"] > 0
+    out = paged_decode_attention(q, cache)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache), label="auto partition skewed")
