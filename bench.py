@@ -325,7 +325,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     if split:
         sk, pps = split, 0
     else:
-        sk, pps = decode_partition(len(lens), hq, hkv, maxp, total_pages)
+        sk, pps = decode_partition(len(lens), hq, hkv, maxp, total_pages, quantized=bool(quant))
     out = torch.empty_like(q)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens), hq, d, sk)), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)

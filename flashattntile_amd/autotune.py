@@ -28,6 +28,7 @@ __all__ = [
     "arithmetic_intensity",
     "decode_split_k",
     "decode_partition",
+    "decode_heads_per_workgroup",
     "MI355X_CUS",
 ]
 
@@ -125,9 +126,18 @@ def decode_split_k(batch: int, num_heads: int, num_kv_heads: int, max_pages: int
     return int(max(1, split))
 
 
+def decode_heads_per_workgroup(group: int, quantized: bool = False) -> int:
+    """Query heads one decode workgroup serves: the MFMA decode (every int8 /
+    fp8 cache, and fp16/bf16 caches with group >= 8) takes up to 32, the VALU
+    decode (fp16/bf16, group < 8) 4."""
+    if quantized or group >= 8:
+        return 32
+    return 4
+
+
 def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: int, total_pages: int,
                      num_cus: int = MI355X_CUS, min_pages_per_split: int = 8,
-                     max_split: int = 16) -> tuple[int, int]:
+                     max_split: int = 16, quantized: bool = False) -> tuple[int, int]:
     """``(split_k, pages_per_split)`` for a possibly ragged batch on MI355X.
 
     Every partition holds the same number of pages and split_k covers the
@@ -141,7 +151,7 @@ def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: i
     lengths in [16, 65536]).
     """
     group = max(1, num_heads // max(1, num_kv_heads))
-    heads_per_wg = 8 if group >= 8 else 4
+    heads_per_wg = decode_heads_per_workgroup(group, quantized)
     groups = num_kv_heads * math.ceil(group / heads_per_wg)
     max_pages = max(1, int(max_pages))
     total_pages = max(1, int(total_pages))

@@ -24,12 +24,27 @@
 //     and a second kernel merges the partitions by log-sum-exp.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
 
 #include "fat_common.h"
 
 namespace fat {
 
 enum KvKind { KV_SAME = 0, KV_I8 = 1, KV_FP8 = 2 };
+
+// Lazy rescale bound of the MFMA decode (log2 units): m only moves when a
+// block's max exceeds it by more than this; p then stays below 2^kDecLazy.
+constexpr float kDecLazy = 8.0f;
+
+// fp16/bf16 K/V with at least this many query heads per KV head use the MFMA
+// decode (FAT_DECODE_KERNEL=valu|mfma overrides the choice).
+constexpr int kDecMfmaMinGroup = 8;
+#ifndef FAT_DEC_MFMA_8BIT
+#define FAT_DEC_MFMA_8BIT 1
+#endif
 
 struct DecodeParams {
   const uint8_t* q;
@@ -393,6 +408,261 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA decode for large GQA groups (group >= 8, e.g. MQA 32/1): one workgroup
+// per (partition, KV head, up to 32 of its query heads, sequence).  With G
+// query heads per KV head every K/V byte feeds 2G FLOPs, more than the VALU
+// sustains at HBM speed for G >= 8, so both products run on the matrix core:
+//   S^T = K Q^T   v_mfma_f32_32x32x16: A = 32 keys x 16 dims straight from
+//                 each lane's own 16-byte K loads (the head dims are permuted
+//                 identically in K and Q so those loads stay contiguous),
+//                 B = Q^T of the 32 heads (registers, loaded once);
+//   O^T += V^T P^T  A = V^T through the wave's LDS tile (ds_read_b64_tr_b16),
+//                 B = P^T straight from the S^T accumulator.
+// Each wave streams its own 32-key blocks (wave-private LDS, no workgroup
+// barrier in the loop) with its own online softmax; the waves merge at the
+// end, and partitions go through the same log-sum-exp merge as the VALU
+// kernel.  P is rounded to the K/V type for PV (bf16: hi + lo parts).
+// ---------------------------------------------------------------------------
+constexpr int kDecMfmaWaves = 4;
+
+template <typename QT, int KV, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void paged_decode_mfma_kernel(const DecodeParams p) {
+  constexpr int NW = kDecMfmaWaves;
+  constexpr int KS = D / 16;     // MFMA k-steps (= 16-byte K loads per lane)
+  constexpr int DB = D / 32;     // 32-dim blocks of O^T
+  constexpr int HALF = D / 2;    // head dims owned by each lane half
+  constexpr int V_RS = D + 32;   // LDS row stride of the V tile (elements)
+  constexpr bool SPLIT_P = std::is_same<QT, BF16>::value;
+  static_assert(KS * 8 == HALF, "lane loads must cover the half row");
+  constexpr int EB = KV == KV_SAME ? 2 : 1;        // bytes per stored element
+  constexpr int NLD = HALF * EB / 16;              // 16-byte loads per lane per row half
+
+  // V tiles during the loop; per-wave O / m / l for the final merge after it.
+  constexpr int kTileBytes = NW * 32 * V_RS * 2;
+  constexpr int kMergeBytes = (NW * 32 * D + NW * 32 * 2) * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes];
+
+  const int split = blockIdx.x;
+  const int S = gridDim.x;
+  const int y = blockIdx.y;
+  const int b = blockIdx.z;
+  const int sub = y % p.hg_per_kv;
+  const int kvh = y / p.hg_per_kv;
+  const int head0 = kvh * p.group + sub * 32;
+  const int nvalid = min(32, p.group - sub * 32);
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 31;  // key row (A operand) / head column (B, S^T)
+  const int g = lane >> 5;   // k-group: head dims [g * HALF, g * HALF + HALF)
+
+  int seq_len = p.lens[b];
+  seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
+  const int np = (seq_len + p.P - 1) >> p.log2P;
+  const int pps = p.pps_fixed > 0 ? p.pps_fixed : (np + S - 1) / S;
+  const int pb = split * pps;
+  const int pe = split == S - 1 ? np : min(np, pb + pps);
+  const int t_begin = pb << p.log2P;
+  const int t_end = min(seq_len, pe << p.log2P);
+  const int n_blocks = t_end > t_begin ? (t_end - t_begin + 31) >> 5 : 0;
+
+  // Q^T: lane (head li, k-group g), k-step ks = head dims g*HALF + 8ks + 0..7.
+  u32x4 qf[KS];
+  {
+    const int qh = head0 + min(li, nvalid - 1);
+    const uint8_t* qp = p.q + 2 * ((int64_t)b * p.q_sb + (int64_t)qh * p.q_sh + g * HALF);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
+  }
+
+  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
+  // Raw K/V bytes of key (block base + li), head dims g*HALF.. (NLD
+  // contiguous 16-byte loads each) and, for 8-bit caches, that key's page
+  // scales.
+  struct Raw {
+    u32x4 k[NLD], v[NLD];
+    float ksc, vsc;
+  };
+  auto fetch = [&](Raw& R, int blk) {
+    const int key = min(t_begin + (blk << 5) + li, t_end - 1);
+    int phys = ptrow[key >> p.log2P];
+    phys = min(max(phys, 0), p.num_pages - 1);
+    const int slot = key & (p.P - 1);
+    const uint8_t* kp = p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + (int64_t)kvh * p.k_sh + g * HALF);
+    const uint8_t* vp = p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + (int64_t)kvh * p.v_sh + g * HALF);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      R.k[j] = *reinterpret_cast<const u32x4*>(kp + 16 * j);
+      R.v[j] = *reinterpret_cast<const u32x4*>(vp + 16 * j);
+    }
+    if constexpr (KV != KV_SAME) {
+      R.ksc = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+      R.vsc = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+    } else {
+      R.ksc = R.vsc = 1.f;
+    }
+  };
+  // MFMA operand words (QT pairs) of k-step ks from the raw bytes: copied for
+  // fp16/bf16 caches, round_to_QT(float(x) * scale) for 8-bit ones.
+  auto operand = [&](const u32x4* raw, float sc, int ks) -> u32x4 {
+    if constexpr (KV == KV_SAME) {
+      return raw[ks];
+    } else {
+      const u32 w0 = raw[ks >> 1][2 * (ks & 1)];
+      const u32 w1 = raw[ks >> 1][2 * (ks & 1) + 1];
+      float f[8];
+      if constexpr (KV == KV_I8) {
+        const float nb = -128.0f * sc;
+        i8x4_biased(w0, f);
+        i8x4_biased(w1, f + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], sc, nb);
+      } else {
+        fp8x4(w0, f);
+        fp8x4(w1, f + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = f[e] * sc;
+      }
+      u32x4 o;
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) o[e2] = Pair<QT>::pack(f[2 * e2], f[2 * e2 + 1]);
+      return o;
+    }
+  };
+
+  uint16_t* const Vt = reinterpret_cast<uint16_t*>(smem) + w * 32 * V_RS;
+  const int tr_c = (lane & 15) >> 2;
+  const int tr_j = lane & 3;
+  const int tr_G = lane >> 4;
+  const int tr_row = 4 * (tr_G >> 1) + tr_c;
+  const int tr_col = 16 * (tr_G & 1) + 4 * tr_j;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  float m_run = -INFINITY;  // log2 units
+  float l_run = 0.f;
+  const float c = p.scale_log2;
+
+  // One 32-key block from R; refills R with block nxt once R is consumed.
+  auto compute = [&](Raw& R, int blk, int nxt) {
+    // V(blk) into this wave's LDS tile (row = key, columns = head dims).
+#pragma unroll
+    for (int j = 0; j < KS; ++j)
+      *reinterpret_cast<u32x4*>(&Vt[li * V_RS + g * HALF + 8 * j]) = operand(R.v, R.vsc, j);
+    // S^T = K Q^T for the 32 keys of this block.
+    u32x4 kop[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kop[ks] = operand(R.k, R.ksc, ks);
+    if (nxt < n_blocks) fetch(R, nxt);  // R is free once its K/V operands are built
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) s = Mfma<QT>::mma(kop[ks], qf[ks], s);
+
+    // Online softmax for head li over keys kb + (r&3) + 4g + 8(r>>2).
+    const int kb = t_begin + (blk << 5);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb + (r & 3) + 4 * g + 8 * (r >> 2);
+      const float x = key < t_end ? s[r] * c : -INFINITY;
+      s[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = xor32<OpMax>(mx);
+    if (__any(mx > m_run + kDecLazy)) {
+      const bool grow = mx > m_run + kDecLazy;
+      const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
+      m_run = grow ? mx : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+    }
+    u32x4 pf[2], pl[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const float x0 = fast_exp2(s[8 * t + 2 * e2] - m_run);
+        const float x1 = fast_exp2(s[8 * t + 2 * e2 + 1] - m_run);
+        l_run += x0 + x1;
+        const u32 hp = Pair<QT>::pack(x0, x1);
+        pf[t][e2] = hp;
+        if constexpr (SPLIT_P) pl[t][e2] = Pair<QT>::pack(x0 - Pair<QT>::lo(hp), x1 - Pair<QT>::hi(hp));
+      }
+    wave_lds_fence();
+    // O^T += V^T P^T (k-step t covers keys 16t..16t+15 of the block).
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int vrow = 16 * t + tr_row;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const uint16_t* vp = &Vt[vrow * V_RS + 32 * db + tr_col];
+        const u32x2 lo = lds_read_tr16(vp);
+        const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
+        const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
+        acc[db] = Mfma<QT>::mma(a, pf[t], acc[db]);
+        if constexpr (SPLIT_P) acc[db] = Mfma<QT>::mma(a, pl[t], acc[db]);
+      }
+    }
+    wave_lds_fence();
+  };
+  Raw R;
+  if (w < n_blocks) fetch(R, w);
+  for (int blk = w; blk < n_blocks; blk += NW) compute(R, blk, blk + NW);
+
+  // ---- merge the waves: O = sum_w acc_w 2^(m_w - M) / sum_w l_w 2^(m_w - M) ----
+  __syncthreads();  // every wave is done with its V tile (smem is reused)
+  float* so = reinterpret_cast<float*>(smem);   // [NW][32 heads][D]
+  float* sml = so + NW * 32 * D;                // [NW][32 heads][2]
+  const float l_tot = xor32<OpAdd>(l_run);
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) so[(w * 32 + li) * D + 32 * db + (r & 3) + 4 * g + 8 * (r >> 2)] = acc[db][r];
+  if (g == 0) {
+    sml[(w * 32 + li) * 2 + 0] = m_run;
+    sml[(w * 32 + li) * 2 + 1] = l_tot;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < nvalid * D; idx += NW * 64) {
+    const int hh = idx / D;
+    const int d = idx - hh * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sml[(ww * 32 + hh) * 2]);
+    float A = 0.f, L = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        const float f = fast_exp2(sml[(ww * 32 + hh) * 2] - M);
+        A = __builtin_fmaf(so[(ww * 32 + hh) * D + d], f, A);
+        L = __builtin_fmaf(sml[(ww * 32 + hh) * 2 + 1], f, L);
+      }
+    }
+    const int h = head0 + hh;
+    if (S == 1) {
+      uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + (b * p.o_sb + h * p.o_sh + d);
+      *op = Pair<QT>::from_float(L > 0.f ? A / L : 0.f);
+    } else {
+      const int64_t row = ((int64_t)b * p.H + h) * S + split;
+      p.ws_acc[row * D + d] = A;
+      if (d == 0) {
+        p.ws_ml[row * 2 + 0] = M;
+        p.ws_ml[row * 2 + 1] = L;
+      }
+    }
+  }
+}
+
 // Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
 //   M = max_s m_s, w_s = 2^(m_s - M), o = sum_s acc_s w_s / sum_s l_s w_s.
 template <typename QT>
@@ -465,6 +735,35 @@ int launch_decode_q(const fat::DecodeParams& prm, int kv, int D, int HG, int nw,
     case fat::KV_I8: return launch_decode_kv<QT, fat::KV_I8>(prm, D, HG, nw, grid, stream);
     default: return launch_decode_kv<QT, fat::KV_FP8>(prm, D, HG, nw, grid, stream);
   }
+}
+
+
+template <typename QT, int KV>
+void launch_decode_mfma_kv(const fat::DecodeParams& prm, int D, dim3 grid, hipStream_t stream) {
+  if (D == 128) hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 128>), grid, dim3(256), 0, stream, prm);
+  else hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 64>), grid, dim3(256), 0, stream, prm);
+}
+
+template <typename QT>
+void launch_decode_mfma_q(const fat::DecodeParams& prm, int kv, int D, dim3 grid, hipStream_t stream) {
+  switch (kv) {
+    case fat::KV_SAME: launch_decode_mfma_kv<QT, fat::KV_SAME>(prm, D, grid, stream); break;
+    case fat::KV_I8: launch_decode_mfma_kv<QT, fat::KV_I8>(prm, D, grid, stream); break;
+    default: launch_decode_mfma_kv<QT, fat::KV_FP8>(prm, D, grid, stream); break;
+  }
+}
+
+int launch_merge(const fat::DecodeParams& prm, const fat_decode_args* a, int D, hipStream_t stream) {
+  const int64_t n = (int64_t)a->batch * a->num_heads * D;
+  const dim3 mgrid((unsigned)((n + 255) / 256));
+  if (a->q_dtype == FAT_DTYPE_F16) {
+    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::F16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
+                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+  } else {
+    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::BF16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
+                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+  }
+  return fat_host::launch_status("decode_merge_kernel");
 }
 
 }  // namespace
@@ -551,7 +850,12 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   }
 
   const int group = a->num_heads / a->num_kv_heads;
-  const int HG = group >= 8 ? 8 : 4;
+  bool use_mfma = group >= fat::kDecMfmaMinGroup || (kv != fat::KV_SAME && FAT_DEC_MFMA_8BIT);
+  if (const char* force = getenv("FAT_DECODE_KERNEL")) {
+    if (!strcmp(force, "mfma")) use_mfma = true;
+    else if (!strcmp(force, "valu")) use_mfma = false;
+  }
+  const int HG = use_mfma ? 32 : (group >= 8 ? 8 : 4);
   const int hg_per_kv = (group + HG - 1) / HG;
 
   fat::DecodeParams prm{};
@@ -592,6 +896,13 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const dim3 grid(a->split_k, a->num_kv_heads * hg_per_kv, a->batch);
+  if (use_mfma) {
+    if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, grid, stream);
+    else launch_decode_mfma_q<fat::BF16>(prm, kv, D, grid, stream);
+    const int rc = fat_host::launch_status("paged_decode_mfma_kernel");
+    if (rc != FAT_OK || a->split_k == 1) return rc;
+    return launch_merge(prm, a, D, stream);
+  }
   // Fewer than two 4-wave workgroups per CU leave the MI355X's 256 CUs short
   // of loads in flight; use 8-wave workgroups then.
   const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
@@ -600,14 +911,5 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
                                          : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);
   if (rc != FAT_OK || a->split_k == 1) return rc;
 
-  const int64_t n = (int64_t)a->batch * a->num_heads * D;
-  const dim3 mgrid((unsigned)((n + 255) / 256));
-  if (a->q_dtype == FAT_DTYPE_F16) {
-    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::F16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
-  } else {
-    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::BF16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
-  }
-  return fat_host::launch_status("decode_merge_kernel");
+  return launch_merge(prm, a, D, stream);
 }

@@ -49,31 +49,6 @@ struct PrefillParams {
   float scale_log2;
 };
 
-template <typename T> struct Mfma;
-template <> struct Mfma<F16> {
-  static __device__ __forceinline__ f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                  0, 0, 0);
-  }
-};
-template <> struct Mfma<BF16> {
-  static __device__ __forceinline__ f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                   c, 0, 0, 0);
-  }
-};
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// Transposed 64-bit LDS read: inside each 16-lane group, lane l receives
-// element (l % 4) of the 4-element row addressed by lane 4c + l/4, for
-// c = 0..3 (gfx950 ds_read_b64_tr_b16).
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
-
 constexpr int kBM = 128;
 constexpr int kBN = 64;
 // Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.

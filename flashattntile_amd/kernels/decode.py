@@ -61,7 +61,7 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, m
     if resolved["split_k"] is None:
         max_pages = -(-max_len // cache.page_size)
         split, chunk = decode_partition(int(q.shape[0]), int(q.shape[1]), cache.num_kv_heads, max_pages,
-                                        total_pages)
+                                        total_pages, quantized=cache.k_cache.dtype in _QUANT_DTYPES)
         resolved["split_k"] = split
         if resolved["pages_per_split"] is None:
             resolved["pages_per_split"] = chunk

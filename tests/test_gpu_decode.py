@@ -27,6 +27,14 @@ ODD_LENS = [1, 17, 255, 1000]
 GQA = [(8, 8), (8, 2), (8, 1), (32, 8), (32, 1)]
 
 
+@pytest.fixture(params=["auto", "valu", "mfma"])
+def decode_kernel(request, monkeypatch):
+    """Run with the library's choice and with each decode kernel forced (the
+    MFMA decode serves fp16/bf16 caches; 8-bit caches always take the VALU one)."""
+    monkeypatch.setenv("FAT_DECODE_KERNEL", request.param)
+    return request.param
+
+
 def _case(lens, h, hk, d, P, dtype, seed=0):
     k, v, pt, sl = make_paged(lens, hk, d, P, dtype, seed=seed, device=DEV)
     q = make_query(len(lens), h, d, dtype, seed=seed + 1, device=DEV)
@@ -43,8 +51,8 @@ def _ref32(q, cache, scale=None):
 @pytest.mark.parametrize("h,hk", GQA)
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_decode_matches_oracle(dtype, d, h, hk, page_size, split_k):
-    label = f"decode {dtype} D{d} H{h}/{hk} P{page_size} sk{split_k}"
+def test_decode_matches_oracle(dtype, d, h, hk, page_size, split_k, decode_kernel):
+    label = f"decode {decode_kernel} {dtype} D{d} H{h}/{hk} P{page_size} sk{split_k}"
     print(label, flush=True)
     q, cache = _case(ODD_LENS, h, hk, d, page_size, dtype, seed=d + h + hk)
     out = paged_decode_attention(q, cache, config={"split_k": split_k})
@@ -55,8 +63,8 @@ def test_decode_matches_oracle(dtype, d, h, hk, page_size, split_k):
 
 @pytest.mark.parametrize("page_size", [4, 8, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_decode_page_sizes(dtype, page_size):
-    label = f"decode pages {dtype} P{page_size}"
+def test_decode_page_sizes(dtype, page_size, decode_kernel):
+    label = f"decode {decode_kernel} pages {dtype} P{page_size}"
     print(label, flush=True)
     d = 128 if page_size >= 8 else 128
     lens = [3, 64, 65, 300]
@@ -76,10 +84,11 @@ def test_decode_more_splits_than_pages():
     assert_parity(out, _ref32(q, cache), label="split16")
 
 
-def test_split_k_agreement_and_softmax_scale():
-    print("decode split agreement", flush=True)
+@pytest.mark.parametrize("hk", [8, 1])
+def test_split_k_agreement_and_softmax_scale(hk, decode_kernel):
+    print(f"decode split agreement {decode_kernel} H32/{hk}", flush=True)
     lens = [1, 17, 255, 1000, 4096, 333]
-    q, cache = _case(lens, 32, 8, 128, 16, torch.float16, seed=22)
+    q, cache = _case(lens, 32, hk, 128, 16, torch.float16, seed=22)
     ref = _ref32(q, cache, scale=0.05)
     outs = {}
     for s in (1, 2, 5, 8, 16, 64):
@@ -88,6 +97,9 @@ def test_split_k_agreement_and_softmax_scale():
     for s, o in outs.items():
         assert_parity(o, ref, label=f"scale0.05 sk{s}")
         assert (o.float() - outs[1].float()).abs().max().item() <= 2e-3
+    neg = paged_decode_attention(q, cache, softmax_scale=-0.05, config={"split_k": 3})
+    torch.cuda.synchronize()
+    assert_parity(neg, _ref32(q, cache, scale=-0.05), label="negative scale")
 
 
 def _quant_case(lens, h, hk, d, P, qdtype, mode, seed):
@@ -107,8 +119,8 @@ def _quant_case(lens, h, hk, d, P, qdtype, mode, seed):
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
-def test_quant_decode_matches_dequantized_oracle(mode, qdtype, d, h, hk, split_k):
-    label = f"quant {mode} {qdtype} D{d} H{h}/{hk} sk{split_k}"
+def test_quant_decode_matches_dequantized_oracle(mode, qdtype, d, h, hk, split_k, decode_kernel):
+    label = f"quant {decode_kernel} {mode} {qdtype} D{d} H{h}/{hk} sk{split_k}"
     print(label, flush=True)
     q, cache, scales, ref = _quant_case(ODD_LENS, h, hk, d, 16, qdtype, mode, seed=13 + d)
     out = paged_decode_attention_fp8(q, cache, scales, config={"split_k": split_k})
@@ -160,7 +172,8 @@ def test_long_context_and_skewed_batch():
     assert_parity(out, _ref32(q, cache), label="skewed64")
 
 
-@pytest.mark.parametrize("h,hk,d,P", [(32, 1, 128, 16), (32, 8, 64, 16), (32, 8, 128, 32), (32, 8, 128, 64)])
+@pytest.mark.parametrize("h,hk,d,P", [(32, 1, 128, 16), (32, 8, 64, 16), (32, 8, 128, 32), (32, 8, 128, 64),
+                                      (64, 1, 128, 16), (16, 1, 64, 32), (48, 3, 128, 16)])
 def test_stress_variants(h, hk, d, P):
     label = f"stress H{h}/{hk} D{d} P{P}"
     print(label, flush=True)
