@@ -20,13 +20,14 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum fat_dtype
 DT_F16 = 0
 DT_BF16 = 1
 DT_I8 = 2
 DT_FP8E4M3 = 3
+DT_F32 = 4
 
 EXPORTED_SYMBOLS = (
     "fat_abi_version",
@@ -35,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "fat_paged_decode",
     "fat_prefill_workspace_bytes",
     "fat_prefill_varlen",
+    "fat_quantize_pages",
+    "fat_append_kv",
 )
 
 _c_i64 = ctypes.c_int64
@@ -117,6 +120,75 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class QuantizeArgs(ctypes.Structure):
+    """Mirror of ``fat_quantize_args``."""
+
+    _fields_ = [
+        ("src", _c_vp),
+        ("dst", _c_vp),
+        ("scale", _c_vp),
+        ("src_stride_page", _c_i64),
+        ("src_stride_slot", _c_i64),
+        ("src_stride_head", _c_i64),
+        ("dst_stride_page", _c_i64),
+        ("dst_stride_slot", _c_i64),
+        ("dst_stride_head", _c_i64),
+        ("scale_stride_page", _c_i64),
+        ("scale_stride_head", _c_i64),
+        ("num_pages", _c_i32),
+        ("page_size", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("src_dtype", _c_i32),
+        ("dst_dtype", _c_i32),
+    ]
+
+
+class AppendArgs(ctypes.Structure):
+    """Mirror of ``fat_append_args``."""
+
+    _fields_ = [
+        ("new_k", _c_vp),
+        ("new_v", _c_vp),
+        ("k_cache", _c_vp),
+        ("v_cache", _c_vp),
+        ("quant_k_cache", _c_vp),
+        ("quant_v_cache", _c_vp),
+        ("k_scale", _c_vp),
+        ("v_scale", _c_vp),
+        ("page_table", _c_vp),
+        ("seq_lens", _c_vp),
+        ("new_k_stride_b", _c_i64),
+        ("new_k_stride_h", _c_i64),
+        ("new_v_stride_b", _c_i64),
+        ("new_v_stride_h", _c_i64),
+        ("k_stride_page", _c_i64),
+        ("k_stride_slot", _c_i64),
+        ("k_stride_head", _c_i64),
+        ("v_stride_page", _c_i64),
+        ("v_stride_slot", _c_i64),
+        ("v_stride_head", _c_i64),
+        ("qk_stride_page", _c_i64),
+        ("qk_stride_slot", _c_i64),
+        ("qk_stride_head", _c_i64),
+        ("qv_stride_page", _c_i64),
+        ("qv_stride_slot", _c_i64),
+        ("qv_stride_head", _c_i64),
+        ("scale_stride_page", _c_i64),
+        ("scale_stride_head", _c_i64),
+        ("page_table_stride", _c_i64),
+        ("batch", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("page_size", _c_i32),
+        ("num_pages", _c_i32),
+        ("max_pages", _c_i32),
+        ("dtype", _c_i32),
+        ("quant_dtype", _c_i32),
+        ("advance", _c_i32),
+    ]
+
+
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
 _ERROR: str | None = None
@@ -150,6 +222,10 @@ def _load() -> None:
         lib.fat_prefill_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32]
         lib.fat_prefill_varlen.restype = ctypes.c_int
         lib.fat_prefill_varlen.argtypes = [ctypes.POINTER(PrefillArgs), _c_vp]
+        lib.fat_quantize_pages.restype = ctypes.c_int
+        lib.fat_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), _c_vp]
+        lib.fat_append_kv.restype = ctypes.c_int
+        lib.fat_append_kv.argtypes = [ctypes.POINTER(AppendArgs), _c_vp]
         version = lib.fat_abi_version()
         if version != ABI_VERSION:
             _ERROR = f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it"
@@ -186,6 +262,8 @@ def dtype_code(dtype: torch.dtype) -> int:
         return DT_I8
     if dtype == getattr(torch, "float8_e4m3fn", None):
         return DT_FP8E4M3
+    if dtype == torch.float32:
+        return DT_F32
     raise TypeError(f"no HIP kernel element type for {dtype}")
 
 
@@ -303,3 +381,71 @@ def prefill_varlen(
     a.softmax_scale = float(softmax_scale)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
+
+
+def quantize_pages(src: torch.Tensor, dst: torch.Tensor, scale: torch.Tensor, stream: int | None = None) -> None:
+    """Enqueue ``fat_quantize_pages``: ``src`` [pages, P, Hkv, D] fp16/bf16/fp32
+    into int8/fp8 codes ``dst`` (same shape) and fp32 ``scale`` [pages, Hkv]."""
+    a = QuantizeArgs()
+    a.src = _ptr(src)
+    a.dst = _ptr(dst)
+    a.scale = _ptr(scale)
+    a.src_stride_page, a.src_stride_slot, a.src_stride_head = src.stride(0), src.stride(1), src.stride(2)
+    a.dst_stride_page, a.dst_stride_slot, a.dst_stride_head = dst.stride(0), dst.stride(1), dst.stride(2)
+    a.scale_stride_page, a.scale_stride_head = scale.stride(0), scale.stride(1)
+    a.num_pages, a.page_size, a.num_kv_heads, a.head_dim = (int(x) for x in src.shape)
+    a.src_dtype = dtype_code(src.dtype)
+    a.dst_dtype = dtype_code(dst.dtype)
+    handle = current_stream_handle(src.device) if stream is None else stream
+    _check(lib().fat_quantize_pages(ctypes.byref(a), _c_vp(handle)), "fat_quantize_pages")
+
+
+def append_kv(
+    new_k: torch.Tensor,
+    new_v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    page_size: int,
+    quant_k: torch.Tensor | None = None,
+    quant_v: torch.Tensor | None = None,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    advance: bool = True,
+    stream: int | None = None,
+) -> None:
+    """Enqueue ``fat_append_kv`` for already-validated device tensors."""
+    a = AppendArgs()
+    a.new_k = _ptr(new_k)
+    a.new_v = _ptr(new_v)
+    a.k_cache = _ptr(k_cache)
+    a.v_cache = _ptr(v_cache)
+    a.quant_k_cache = _ptr(quant_k)
+    a.quant_v_cache = _ptr(quant_v)
+    a.k_scale = _ptr(k_scale)
+    a.v_scale = _ptr(v_scale)
+    a.page_table = _ptr(page_table)
+    a.seq_lens = _ptr(seq_lens)
+    a.new_k_stride_b, a.new_k_stride_h = new_k.stride(0), new_k.stride(1)
+    a.new_v_stride_b, a.new_v_stride_h = new_v.stride(0), new_v.stride(1)
+    a.k_stride_page, a.k_stride_slot, a.k_stride_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_stride_page, a.v_stride_slot, a.v_stride_head = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    if quant_k is not None:
+        a.qk_stride_page, a.qk_stride_slot, a.qk_stride_head = quant_k.stride(0), quant_k.stride(1), quant_k.stride(2)
+        a.quant_dtype = dtype_code(quant_k.dtype)
+    if quant_v is not None:
+        a.qv_stride_page, a.qv_stride_slot, a.qv_stride_head = quant_v.stride(0), quant_v.stride(1), quant_v.stride(2)
+    if k_scale is not None:
+        a.scale_stride_page, a.scale_stride_head = k_scale.stride(0), k_scale.stride(1)
+    a.page_table_stride = page_table.stride(0)
+    a.batch = new_k.shape[0]
+    a.num_kv_heads = k_cache.shape[2]
+    a.head_dim = k_cache.shape[3]
+    a.page_size = int(page_size)
+    a.num_pages = k_cache.shape[0]
+    a.max_pages = page_table.shape[1]
+    a.dtype = dtype_code(k_cache.dtype)
+    a.advance = 1 if advance else 0
+    handle = current_stream_handle(k_cache.device) if stream is None else stream
+    _check(lib().fat_append_kv(ctypes.byref(a), _c_vp(handle)), "fat_append_kv")

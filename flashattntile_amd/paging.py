@@ -183,10 +183,45 @@ def allocate(
     return cache
 
 
-def append_tokens(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor) -> None:
+def _quant_pair(cache: PagedKVCache, quantized) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Check an int8/fp8 copy ``(qcache, scales)`` of ``cache`` and return
+    ``(qk, qv, k_scale, v_scale)``."""
+    qcache, scales = quantized
+    qk, qv = qcache.k_cache, qcache.v_cache
+    sk = scales["k"] if isinstance(scales, dict) else scales.k
+    sv = scales["v"] if isinstance(scales, dict) else scales.v
+    fp8 = getattr(torch, "float8_e4m3fn", None)
+    shape = tuple(cache.k_cache.shape)
+    _require(tuple(qk.shape) == shape and tuple(qv.shape) == shape,
+             f"quantised pages {tuple(qk.shape)} / {tuple(qv.shape)} must match the cache {shape}")
+    _require(qk.dtype in (torch.int8, fp8) and qv.dtype == qk.dtype,
+             f"quantised pages must be int8 or float8_e4m3fn, got {qk.dtype} / {qv.dtype}")
+    want = (shape[0], shape[2])
+    _require(tuple(sk.shape) == want and tuple(sv.shape) == want,
+             f"scales must be [{want[0]}, {want[1]}], got {tuple(sk.shape)} / {tuple(sv.shape)}")
+    _require(sk.dtype == torch.float32 and sv.dtype == torch.float32, "scales must be float32")
+    dev = cache.k_cache.device
+    _require(all(t.device == dev for t in (qk, qv, sk, sv)), "the quantised copy must live on the cache device")
+    return qk, qv, sk, sv
+
+
+def append_tokens(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor, quantized=None, *,
+                  validate: bool = True) -> None:
     """Write one token per sequence at position ``seq_lens[b]`` through the page
-    table, then increment ``seq_lens`` in place (``paging.py:172-210``)."""
-    validate_cache(cache, check_pages=False)
+    table, then increment ``seq_lens`` in place (``paging.py:172-210``).
+
+    ``quantized``: optional ``(qcache, scales)`` from ``quant.quantize_cache``
+    -- an int8/fp8 copy of this cache under the same page table.  Each
+    (page, KV head) that receives a token is requantised from the updated
+    pages, so the copy stays equal to ``quantize_cache`` of the updated cache
+    (the reference has no incremental form; it requantises the whole cache).
+
+    On a ROCm cache the write (and the requantisation) is the HIP kernel
+    ``fat_append_kv``; the bounds checks cost one device synchronisation.
+    ``validate=False`` skips them (ROCm only): an entry whose position or page
+    id is out of range is then skipped on the device and its length kept.
+    """
+    _check_layout(cache)
     expect = (cache.batch_size, cache.num_kv_heads, cache.head_dim)
     _require(new_k.shape == expect,
              f"new_k must be [{expect[0]}, {expect[1]}, {expect[2]}], got {tuple(new_k.shape)}")
@@ -195,8 +230,15 @@ def append_tokens(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor)
     _require(new_v.dtype == cache.k_cache.dtype, f"new_v dtype {new_v.dtype} != cache dtype {cache.k_cache.dtype}")
     _require(new_k.device == cache.k_cache.device, "new_k must be on the cache device")
     _require(new_v.device == cache.k_cache.device, "new_v must be on the cache device")
+    mirror = _quant_pair(cache, quantized) if quantized is not None else None
+    if cache.k_cache.is_cuda:
+        _append_hip(cache, new_k, new_v, mirror, validate)
+        return
 
+    validate_cache(cache, check_pages=False)
     pos = cache.seq_lens.long()
+    if pos.numel() == 0:
+        return
     block = torch.div(pos, cache.page_size, rounding_mode="floor")
     rows = torch.arange(cache.batch_size, device=cache.page_table.device)
     safe_block = block.clamp(max=cache.max_pages_per_seq - 1)
@@ -211,7 +253,53 @@ def append_tokens(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor)
     phys = phys.to(cache.k_cache.device)
     cache.k_cache[phys, slots] = new_k
     cache.v_cache[phys, slots] = new_v
+    if mirror is not None:
+        from .quant import quantize_kv_pages
+
+        qk, qv, sk, sv = mirror
+        touched = torch.unique(phys)
+        mode = "int8" if qk.dtype == torch.int8 else "float8_e4m3fn"
+        nk, nv, nsk, nsv, _ = quantize_kv_pages(cache.k_cache[touched], cache.v_cache[touched], mode=mode)
+        qk[touched], qv[touched], sk[touched], sv[touched] = nk, nv, nsk, nsv
     cache.seq_lens += 1
+
+
+def _append_hip(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor, mirror, validate: bool) -> None:
+    """ROCm path of :func:`append_tokens`: bounds checks in one copy, then
+    ``fat_append_kv`` on the current stream."""
+    from . import _hip
+
+    dev = cache.k_cache.device
+    _require(cache.page_table.device == dev and cache.seq_lens.device == dev,
+             "page_table and seq_lens must live on the cache device")
+    _require(cache.k_cache.stride(3) == 1 and cache.v_cache.stride(3) == 1, "the head_dim axis must be contiguous")
+    _require(cache.seq_lens.is_contiguous(), "seq_lens must be contiguous (it is advanced in place)")
+    if mirror is not None:
+        _require(mirror[0].stride(3) == 1 and mirror[1].stride(3) == 1,
+                 "the head_dim axis of the quantised pages must be contiguous")
+        _require(mirror[2].stride() == mirror[3].stride(), "k and v scales must share strides")
+    if cache.batch_size == 0:
+        return
+    pt = cache.page_table if cache.page_table.stride(1) == 1 else cache.page_table.contiguous()
+    if validate:
+        pos = cache.seq_lens.long()
+        block = torch.div(pos, cache.page_size, rounding_mode="floor")
+        rows = torch.arange(cache.batch_size, device=dev)
+        phys = pt[rows, block.clamp(0, cache.max_pages_per_seq - 1)]
+        min_len, max_pos, lo, hi = (int(x) for x in torch.stack(
+            [pos.min(), pos.max(), phys.min().long(), phys.max().long()]).cpu().tolist())
+        # Same checks, order and messages as validate_cache + paging.py:192-205.
+        _require(min_len >= 0, "seq_lens must be non-negative")
+        _require(max_pos <= cache.capacity, f"seq_len {max_pos} exceeds page-table capacity {cache.capacity}")
+        _require(max_pos < cache.capacity, f"append would exceed page-table capacity {cache.capacity}")
+        _require(lo >= 0 and hi < cache.num_pages, f"page_table maps to a page outside [0, {cache.num_pages})")
+    nk = new_k if new_k.stride(2) == 1 else new_k.contiguous()
+    nv = new_v if new_v.stride(2) == 1 else new_v.contiguous()
+    qk = qv = sk = sv = None
+    if mirror is not None:
+        qk, qv, sk, sv = mirror
+    _hip.append_kv(nk, nv, cache.k_cache, cache.v_cache, pt, cache.seq_lens, cache.page_size,
+                   quant_k=qk, quant_v=qv, k_scale=sk, v_scale=sv, advance=True)
 
 
 def gather_paged(

@@ -110,16 +110,37 @@ def quantize_kv_pages(
     min_scale = INT8_MIN_SCALE if is_int8 else FP8_MIN_SCALE
     _, page_size, kv_heads, head_dim = k_cache.shape
 
-    def one(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        xf = x.detach().to(torch.float32)
-        scale = (xf.abs().amax(dim=(1, 3)) / max_val).clamp_min(min_scale)
-        y = xf / scale[:, None, :, None]
-        if is_int8:
-            y = torch.round(y)
-        return y.clamp(-max_val, max_val).to(dtype), scale
+    if k_cache.is_cuda:
+        from . import _hip
+
+        def one(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+            # fat_quantize_pages (HIP): fp16/bf16/fp32 pages in, codes and
+            # fp32 scales out; other float types are rounded to fp32 first,
+            # as quant.py:111-112 does.
+            src = x.detach()
+            if src.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+                src = src.to(torch.float32)
+            if src.stride(3) != 1:
+                src = src.contiguous()
+            codes = torch.empty(x.shape, dtype=dtype, device=x.device)
+            scale = torch.empty(x.shape[0], x.shape[2], dtype=torch.float32, device=x.device)
+            _hip.quantize_pages(src, codes, scale)
+            return codes, scale
+    else:
+        def one(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+            xf = x.detach().to(torch.float32)
+            scale = (xf.abs().amax(dim=(1, 3)) / max_val).clamp_min(min_scale)
+            y = xf / scale[:, None, :, None]
+            if is_int8:
+                y = torch.round(y)
+            return y.clamp(-max_val, max_val).to(dtype), scale
 
     qk, k_scale = one(k_cache)
     qv, v_scale = one(v_cache)
+    if k_scale.numel():
+        scale_min, scale_max = (float(x) for x in torch.stack([k_scale.min(), k_scale.max()]).cpu().tolist())
+    else:
+        scale_min = scale_max = 0.0
     info = {
         "mode": mode,
         "dtype": str(qk.dtype),
@@ -129,8 +150,8 @@ def quantize_kv_pages(
         "num_kv_heads": int(kv_heads),
         "head_dim": int(head_dim),
         "scale_dtype": str(k_scale.dtype),
-        "scale_min": float(k_scale.min().item()) if k_scale.numel() else 0.0,
-        "scale_max": float(k_scale.max().item()) if k_scale.numel() else 0.0,
+        "scale_min": scale_min,
+        "scale_max": scale_max,
         "rounding": "round-to-nearest" if is_int8 else "cast-to-fp8",
     }
     return qk, qv, k_scale, v_scale, info

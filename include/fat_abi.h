@@ -22,6 +22,11 @@
  *                          (paged_decode_attention_fp8: _decode_paged_quant_kernel)
  *   fat_prefill_varlen     flashattn_tile/kernels/prefill.py:236-326
  *                          (prefill_attention: _fwd_varlen_kernel)
+ *   fat_quantize_pages     flashattn_tile/quant.py:84-142
+ *                          (quantize_kv_pages, one of K or V per call)
+ *   fat_append_kv          flashattn_tile/paging.py:172-210
+ *                          (append_tokens), plus the requantisation of the
+ *                          touched pages of an int8/fp8 copy of the cache
  */
 #ifndef FAT_ABI_H
 #define FAT_ABI_H
@@ -33,14 +38,15 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 2
+#define FAT_ABI_VERSION 3
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
   FAT_DTYPE_F16 = 0,     /* IEEE binary16                                  */
   FAT_DTYPE_BF16 = 1,    /* bfloat16                                       */
   FAT_DTYPE_I8 = 2,      /* symmetric int8 KV storage (scale = absmax/127) */
-  FAT_DTYPE_FP8E4M3 = 3  /* OCP float8 e4m3fn KV storage (absmax/448)      */
+  FAT_DTYPE_FP8E4M3 = 3, /* OCP float8 e4m3fn KV storage (absmax/448)      */
+  FAT_DTYPE_F32 = 4      /* IEEE binary32 (fat_quantize_pages source only) */
 };
 
 /* Error codes. */
@@ -148,6 +154,80 @@ typedef struct fat_prefill_args {
   float softmax_scale;
 } fat_prefill_args;
 
+/*
+ * Per-(page, KV head) quantisation of a paged cache tensor.
+ *   src   [num_pages, page_size, num_kv_heads, head_dim]  src_dtype
+ *   dst   same shape                                       dst_dtype
+ *   scale fp32 [num_pages, num_kv_heads]
+ * For every (page, head): scale = max(absmax over (slot, dim) / qmax, 1e-8)
+ * with qmax = 127 (int8) or 448 (fp8); the division is correctly rounded.
+ * int8 codes are clamp(round_half_even(x / scale), -127, 127); fp8 codes are
+ * clamp(x / scale, -448, 448) rounded to nearest-even e4m3fn
+ * (flashattn_tile/quant.py:114-127).  Strides are in elements and head_dim is
+ * contiguous.  Source values must be finite.
+ */
+typedef struct fat_quantize_args {
+  const void* src;
+  void* dst;
+  float* scale;
+  int64_t src_stride_page, src_stride_slot, src_stride_head;
+  int64_t dst_stride_page, dst_stride_slot, dst_stride_head;
+  int64_t scale_stride_page, scale_stride_head;
+  int32_t num_pages;
+  int32_t page_size;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t src_dtype; /* FAT_DTYPE_F16, FAT_DTYPE_BF16 or FAT_DTYPE_F32 */
+  int32_t dst_dtype; /* FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3 */
+} fat_quantize_args;
+
+/*
+ * Append one token per sequence to a paged cache (and its quantised copy).
+ *   new_k, new_v   [batch, num_kv_heads, head_dim]       dtype
+ *   k_cache, v_cache [num_pages, page_size, num_kv_heads, head_dim]  dtype
+ *   page_table     int32 [batch, max_pages], seq_lens int32 [batch]
+ * Token b goes to slot seq_lens[b] % page_size of page
+ * page_table[b, seq_lens[b] / page_size].  With advance != 0, seq_lens[b]
+ * is incremented after every write of the call is done.
+ * Optional quantised copy (quant_k_cache/quant_v_cache non-NULL, int8 or fp8
+ * pages with fp32 scales [num_pages, num_kv_heads]): every (page, KV head)
+ * that received a token is requantised from the updated dtype page, so the
+ * copy holds what fat_quantize_pages of the whole updated cache would give.
+ * The caller guarantees 0 <= seq_lens[b] < max_pages * page_size and page
+ * ids in [0, num_pages) (flashattn_tile/paging.py:192-205 checks this on the
+ * host); an entry that breaks it is skipped, never written out of bounds.
+ * Several sequences may append into the same page (distinct slots).
+ */
+typedef struct fat_append_args {
+  const void* new_k;
+  const void* new_v;
+  void* k_cache;
+  void* v_cache;
+  void* quant_k_cache;
+  void* quant_v_cache;
+  float* k_scale;
+  float* v_scale;
+  const int32_t* page_table;
+  int32_t* seq_lens;
+  int64_t new_k_stride_b, new_k_stride_h;
+  int64_t new_v_stride_b, new_v_stride_h;
+  int64_t k_stride_page, k_stride_slot, k_stride_head;
+  int64_t v_stride_page, v_stride_slot, v_stride_head;
+  int64_t qk_stride_page, qk_stride_slot, qk_stride_head;
+  int64_t qv_stride_page, qv_stride_slot, qv_stride_head;
+  int64_t scale_stride_page, scale_stride_head; /* shared by k/v_scale */
+  int64_t page_table_stride;
+  int32_t batch;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t num_pages;
+  int32_t max_pages;
+  int32_t dtype;       /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
+  int32_t quant_dtype; /* FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3 (with a copy) */
+  int32_t advance;     /* 1 = seq_lens += 1 (the reference's behaviour)   */
+} fat_append_args;
+
 /* ABI version of the loaded library (FAT_ABI_VERSION at build time). */
 int fat_abi_version(void);
 
@@ -169,6 +249,14 @@ size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
 /* Enqueue varlen prefill on `stream`.
  * Replaces flashattn_tile/kernels/prefill.py:236-326 (see file header). */
 int fat_prefill_varlen(const fat_prefill_args* args, void* stream);
+
+/* Enqueue the quantisation of one paged K or V tensor on `stream`.
+ * Replaces flashattn_tile/quant.py:84-142 (quantize_kv_pages). */
+int fat_quantize_pages(const fat_quantize_args* args, void* stream);
+
+/* Enqueue a one-token-per-sequence append on `stream`.
+ * Replaces flashattn_tile/paging.py:172-210 (append_tokens). */
+int fat_append_kv(const fat_append_args* args, void* stream);
 
 #ifdef __cplusplus
 }

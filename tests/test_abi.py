@@ -51,6 +51,8 @@ def test_struct_layout_matches_ctypes(tmp_path):
     fields = {
         "fat_decode_args": [f for f, _ in _hip.DecodeArgs._fields_],
         "fat_prefill_args": [f for f, _ in _hip.PrefillArgs._fields_],
+        "fat_quantize_args": [f for f, _ in _hip.QuantizeArgs._fields_],
+        "fat_append_args": [f for f, _ in _hip.AppendArgs._fields_],
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for struct, names in fields.items():
@@ -65,7 +67,8 @@ def test_struct_layout_matches_ctypes(tmp_path):
     for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
         struct, name, val = line.split()
         got[(struct, name)] = int(val)
-    for struct, cls in (("fat_decode_args", _hip.DecodeArgs), ("fat_prefill_args", _hip.PrefillArgs)):
+    for struct, cls in (("fat_decode_args", _hip.DecodeArgs), ("fat_prefill_args", _hip.PrefillArgs),
+                        ("fat_quantize_args", _hip.QuantizeArgs), ("fat_append_args", _hip.AppendArgs)):
         assert got[(struct, "size")] == ctypes.sizeof(cls)
         for n, _ in cls._fields_:
             assert got[(struct, n)] == getattr(cls, n).offset, (struct, n)
@@ -117,3 +120,46 @@ def test_prefill_argument_errors_are_reported():
     a = _hip.PrefillArgs()
     assert lib.fat_prefill_varlen(ctypes.byref(a), None) != 0
     assert _err()
+
+
+def test_quantize_argument_errors_are_reported():
+    lib = _hip.lib()
+    assert lib.fat_quantize_pages(None, None) == 1 and "required" in _err()
+    a = _hip.QuantizeArgs()
+    a.src, a.dst, a.scale = 0x1000, 0x2000, 0x3000
+    a.num_pages, a.page_size, a.num_kv_heads, a.head_dim = 1, 0, 1, 128
+    assert lib.fat_quantize_pages(ctypes.byref(a), None) == 1 and "positive" in _err()
+    a.page_size = 16
+    a.src_dtype, a.dst_dtype = _hip.DT_F16, _hip.DT_F16
+    assert lib.fat_quantize_pages(ctypes.byref(a), None) == 2 and "dst_dtype" in _err()
+    a.src_dtype, a.dst_dtype = _hip.DT_I8, _hip.DT_I8
+    assert lib.fat_quantize_pages(ctypes.byref(a), None) == 2 and "src_dtype" in _err()
+    # No pages: nothing to launch, success.
+    a.src_dtype, a.num_pages = _hip.DT_F32, 0
+    assert lib.fat_quantize_pages(ctypes.byref(a), None) == 0 and _err() == ""
+
+
+def test_append_argument_errors_are_reported():
+    lib = _hip.lib()
+    assert lib.fat_append_kv(None, None) == 1 and "required" in _err()
+    a = _hip.AppendArgs()
+    for f in ("new_k", "new_v", "k_cache", "v_cache", "page_table", "seq_lens"):
+        setattr(a, f, 0x1000)
+    a.batch, a.num_kv_heads, a.head_dim, a.page_size, a.num_pages, a.max_pages = 2, 2, 128, 16, 0, 4
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 1 and "positive" in _err()
+    a.num_pages = 8
+    a.max_pages = 1 << 28
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 1 and "overflows" in _err()
+    a.max_pages = 4
+    a.dtype = _hip.DT_I8
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 2 and "fp16 or bf16" in _err()
+    a.dtype = _hip.DT_BF16
+    a.quant_k_cache = 0x4000  # a quantised copy needs both code tensors and both scales
+    a.quant_dtype = _hip.DT_I8
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 1 and "quantised copy" in _err()
+    a.quant_v_cache, a.k_scale, a.v_scale = 0x5000, 0x6000, 0x7000
+    a.quant_dtype = _hip.DT_F16
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 1 and "quantised copy" in _err()
+    # Empty batch: nothing to launch, success.
+    a.quant_dtype, a.batch = _hip.DT_FP8E4M3, 0
+    assert lib.fat_append_kv(ctypes.byref(a), None) == 0 and _err() == ""

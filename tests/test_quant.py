@@ -98,3 +98,57 @@ def test_modes_and_errors():
     with pytest.raises(ValueError, match="scale_k shape"):
         quant.dequantize_kv_pages(torch.zeros(2, 2, 1, 2, dtype=torch.int8), torch.zeros(2, 2, 1, 2, dtype=torch.int8),
                                   torch.ones(3, 1), torch.ones(3, 1))
+
+
+def _nearest_even_fp8(y: float, table: torch.Tensor) -> int:
+    """Brute force: among the finite e4m3fn codes with the sign of y (rounding
+    keeps the sign, also for results of zero), the one nearest to y; a tie
+    goes to the even code (round to nearest even)."""
+    sign = 0x80 if math.copysign(1.0, y) < 0 else 0x00
+    same = [c for c in range(256) if (c & 0x80) == sign and not math.isnan(table[c].item())]
+    best = min(abs(table[c].item() - y) for c in same)
+    cands = [c for c in same if abs(table[c].item() - y) == best]
+    assert len(cands) <= 2
+    return min(cands, key=lambda c: c & 1)
+
+
+def test_oracle_fp8_cast_is_round_to_nearest_even():
+    """The oracle's fp8 codes (torch's cast) against a brute-force
+    nearest-even search over the 256-code table, at and beside every rounding
+    midpoint.  The GPU tests then hold the gfx950 conversion to the oracle."""
+    table = quant_ref.fp8_table()
+    pos = table[:0x7F].double()
+    mids = ((pos[1:] + pos[:-1]) / 2).float()
+    vals = torch.cat([pos.float(), mids, torch.nextafter(mids, mids - 1), torch.nextafter(mids, mids + 1),
+                      torch.tensor([2.0 ** -10, 2.0 ** -11, 3 * 2.0 ** -11])])
+    vals = torch.cat([vals, -vals])
+    x = torch.zeros(vals.numel() + 1)
+    x[0] = 448.0  # absmax 448: scale exactly 1
+    x[1:] = vals
+    q, s = quant_ref.quantize_pages(x.view(1, -1, 1, 1), "float8_e4m3fn")
+    assert s.item() == 1.0
+    codes = q.view(torch.uint8).view(-1)[1:].tolist()
+    for y, c in zip(vals.tolist(), codes):
+        assert c == _nearest_even_fp8(y, table), (y, hex(c))
+
+
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+def test_append_with_quantised_copy_cpu(mode):
+    """append_tokens(..., quantized=(qcache, scales)) keeps the copy equal to
+    quantize_cache of the updated cache (CPU tensors: the torch path)."""
+    g = torch.Generator().manual_seed(4)
+    cache = allocate(3, 40, 2, 32, 8, dtype=torch.float16)
+    for _ in range(5):
+        append_tokens(cache, torch.randn(3, 2, 32, generator=g).half(), torch.randn(3, 2, 32, generator=g).half())
+    qc, scales = quant.quantize_cache(cache, mode=mode)
+    for step in range(10):
+        nk = (torch.randn(3, 2, 32, generator=g) * (1 + 4 * (step % 2))).half()
+        nv = torch.randn(3, 2, 32, generator=g).half()
+        append_tokens(cache, nk, nv, quantized=(qc, scales))
+        full, fs = quant.quantize_cache(cache, mode=mode)
+        assert torch.equal(qc.k_cache.view(torch.uint8), full.k_cache.view(torch.uint8))
+        assert torch.equal(qc.v_cache.view(torch.uint8), full.v_cache.view(torch.uint8))
+        assert torch.equal(scales.k, fs.k) and torch.equal(scales.v, fs.v)
+    assert qc.seq_lens is cache.seq_lens and cache.seq_lens.tolist() == [15, 15, 15]
+    with pytest.raises(AssertionError, match="quantised pages"):
+        append_tokens(cache, nk, nv, quantized=(cache, scales))
