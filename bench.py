@@ -273,7 +273,9 @@ def bench_prefill(args, device, seq=8192):
             "ms": round(r["ms"], 4),
             "tflops": round(r["tflops"], 1),
             "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"]},
+                         "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"],
+                         "traffic": (_traffic_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128")
+                                     if name == "f16" else None)},
         }
     res["workload"] = f"prefill_causal_seq{seq}_h32_kv8_d128"
     res["steps"] = steps
@@ -396,6 +398,94 @@ def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
                     "sample": f"{group} query heads / 1 KV head of sequence 0 (L={L}), min of {reps}"}}
 
 
+def _quantize_row(name, src_dtype, mode, device, args, pages=8192, page=16, hkv=8, d=128):
+    """fat_quantize_pages over a whole K pool (the headline cache's 8192 pages);
+    two pools alternate.  Bytes = read src + write codes + write scales."""
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd import _hip
+    from oracle.quant_ref import quantize_pages
+
+    gen = torch.Generator(device=device).manual_seed(5)
+    srcs = [torch.randn(pages, page, hkv, d, device=device, generator=gen).to(src_dtype) for _ in range(2)]
+    qdt = torch.int8 if mode == "int8" else torch.float8_e4m3fn
+    codes = torch.empty(pages, page, hkv, d, dtype=qdt, device=device)
+    scale = torch.empty(pages, hkv, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device)
+    handle = int(stream.cuda_stream)
+
+    def step(i):
+        _hip.quantize_pages(srcs[i % 2], codes, scale, stream=handle)
+
+    ms = _time_steps(step, max(20, args.steps // 4), 5, stream)
+    elem = srcs[0].element_size()
+    nbytes = pages * page * hkv * d * (elem + 1) + pages * hkv * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    sample = srcs[0][:256].cpu()
+    best, reps = _time_cpu(lambda: quantize_pages(sample, mode), args.cpu_budget / 4)
+    cpu_bytes = 256 * page * hkv * d * (elem + 1) + 256 * hkv * 4
+    del srcs
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "kv_write", "value": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes,
+            "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
+                    "sample": f"256 of {pages} pages, min of {reps}"}}
+
+
+def _append_row(name, mode, device, args, B=32, ctx=4000, page=16, hkv=8, d=128):
+    """append_tokens (HIP, validate=False: no host sync) of one token per
+    sequence into the headline-shaped cache, optionally keeping an fp8/int8
+    copy requantised; latency per call.  Bytes = rows written + touched
+    (page, head) units re-read and re-quantised."""
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd.paging import PagedKVCache, append_tokens
+    from flashattntile_amd.quant import quantize_cache
+
+    maxp = (ctx + 64) // page + 1
+    gen = torch.Generator(device=device).manual_seed(6)
+    k = torch.randn(B * maxp, page, hkv, d, device=device, generator=gen).half()
+    v = torch.randn_like(k)
+    perm = torch.randperm(B * maxp, device=device, generator=gen).to(torch.int32)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=device)
+    cache = PagedKVCache(k, v, perm.view(B, maxp), lens, page)
+    mirror = quantize_cache(cache, mode=mode) if mode else None
+    nk = torch.randn(B, hkv, d, device=device, generator=gen).half()
+    nv = torch.randn_like(nk)
+    stream = torch.cuda.current_stream(device)
+
+    def step(i):
+        if i % 64 == 0:
+            lens.fill_(ctx)  # stay inside the table (64 appends per refill)
+        append_tokens(cache, nk, nv, quantized=mirror, validate=False)
+
+    steps = max(64, args.steps // 2)
+    ms = _time_steps(step, steps, 8, stream)
+    nbytes = 2 * B * hkv * d * 2
+    if mode:
+        nbytes += 2 * B * hkv * (page * d * (2 + 1) + 4)
+    # CPU: the torch path of append_tokens on a CPU copy of 4 sequences (no copy maintained)
+    kc = k[: 4 * maxp].cpu()
+    vc = v[: 4 * maxp].cpu()
+    tab = torch.arange(4 * maxp, dtype=torch.int32).view(4, maxp)
+    lc = torch.full((4,), ctx, dtype=torch.int32)
+    ccache = PagedKVCache(kc, vc, tab, lc, page)
+    nkc, nvc = nk[:4].cpu(), nv[:4].cpu()
+
+    def cpu_step():
+        lc.fill_(ctx)
+        append_tokens(ccache, nkc, nvc)
+
+    best, reps = _time_cpu(cpu_step, args.cpu_budget / 8)
+    del cache, mirror, k, v
+    torch.cuda.empty_cache()
+    us = ms * 1e3
+    return {"config": name, "kind": "kv_write", "value": round(us, 2), "unit": "us/call",
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "us": round(us, 2), "bytes": nbytes,
+            "cpu": {"value": round(best * 1e6, 1), "unit": "us/call (torch path, 4 sequences)",
+                    "sample": f"4 of {B} sequences, min of {reps}"}}
+
+
 def all_configs(args, device):
     flush = torch.ones(FLUSH_BYTES // 8, dtype=torch.float64, device=device)
     rows = []
@@ -435,6 +525,13 @@ def all_configs(args, device):
     emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
     for page in (32, 64):
         emit(_decode_row(f"decode fp16 P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device, args, flush))
+    # KV write path (flashattn_tile/quant.py:84-142, paging.py:172-210): quantise the headline
+    # pool; one-token append
+    for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        for mode, mn in (("int8", "int8"), ("float8_e4m3fn", "fp8")):
+            emit(_quantize_row(f"kvwrite quantize {dn}->{mn} 8192 pages", dt, mode, device, args))
+    emit(_append_row("kvwrite append B32", None, device, args))
+    emit(_append_row("kvwrite append B32 + fp8 copy", "float8_e4m3fn", device, args))
     return rows
 
 
