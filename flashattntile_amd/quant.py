@@ -9,7 +9,10 @@ Drop-in for ``flashattn_tile/quant.py`` (same names and semantics):
 * fp8: ``clamp(x / scale, -448, 448).to(float8_e4m3fn)`` (``quant.py:125-127``);
 * dequantise: ``(float(x) * scale).to(out_dtype)`` (``quant.py:145-161``).
 
-The HIP decode kernel applies that dequantisation in registers, so a quantised
+On ROCm tensors the quantisation itself is the HIP kernel ``fat_quantize_pages``
+(one pass over the pages, bit-exact to the formulas above); CPU tensors take
+the torch expressions.  The HIP decode kernels apply the dequantisation in
+registers, so a quantised
 cache costs 1 byte per element of HBM traffic plus 8 bytes of scales per
 (page, KV head).  On gfx950 float8_e4m3fn is the OCP encoding the hardware
 converts natively (v_cvt_pk_f32_fp8), which is why it is the default format
