@@ -398,6 +398,57 @@ def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
                     "sample": f"{group} query heads / 1 KV head of sequence 0 (L={L}), min of {reps}"}}
 
 
+def _paged_prefill_row(name, lens_k, lens_q, dtype, device, args, page=16, hq=32, hkv=8, d=128):
+    """fat_prefill_paged: each sequence's q_len-token chunk attends to its
+    kv_len keys read through the page table (permuted pool)."""
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd import _hip
+    from flashattntile_amd.autotune import flops_attention_varlen
+    from oracle.reference import ref_attention_paged_prefill
+
+    gen = torch.Generator(device=device).manual_seed(12)
+    pages_per = [math.ceil(n / page) for n in lens_k]
+    num_pages = sum(pages_per)
+    k = torch.randn(num_pages, page, hkv, d, device=device, generator=gen).to(dtype)
+    v = torch.randn(num_pages, page, hkv, d, device=device, generator=gen).to(dtype)
+    perm = torch.randperm(num_pages, device=device, generator=gen).to(torch.int32)
+    table = torch.zeros(len(lens_k), max(pages_per), dtype=torch.int32, device=device)
+    at = 0
+    for b, n in enumerate(pages_per):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    seq = torch.tensor(lens_k, dtype=torch.int32, device=device)
+    q = torch.randn(sum(lens_q), hq, d, device=device, generator=gen).to(dtype)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens_q), 0).tolist(), dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(device)
+    handle = int(stream.cuda_stream)
+    mq = max(lens_q)
+
+    def step(i):
+        _hip.prefill_paged(q, k, v, table, seq, cu, out, page, mq, True, d ** -0.5, stream=handle)
+
+    ms = _time_steps(step, max(10, args.steps // 10), 3, stream)
+    flops = flops_attention_varlen(hq, d, lens_q, lens_k, causal=True)
+    tflops = flops / (ms * 1e-3) / 1e12
+    # CPU oracle: one KV head's query heads of the first sequence
+    group = hq // hkv
+    q0 = q[: lens_q[0], :group].cpu()
+    k0 = k[:, :, :1].cpu()
+    v0 = v[:, :, :1].cpu()
+    best, reps = _time_cpu(lambda: ref_attention_paged_prefill(q0, k0, v0, table[:1].cpu(), seq[:1].cpu(),
+                                                               [0, lens_q[0]], causal=True), args.cpu_budget / 4,
+                           max_reps=5)
+    cpu_flops = flops_attention_varlen(group, d, lens_q[:1], lens_k[:1], causal=True)
+    del k, v
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "prefill_paged", "value": round(tflops, 1), "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "us": round(ms * 1e3, 2), "flops": flops,
+            "cpu": {"value": round(cpu_flops / best / 1e12, 5), "unit": "TFLOP/s",
+                    "sample": f"{group} query heads / 1 KV head of sequence 0, min of {reps}"}}
+
+
 def _quantize_row(name, src_dtype, mode, device, args, pages=8192, page=16, hkv=8, d=128):
     """fat_quantize_pages over a whole K pool (the headline cache's 8192 pages);
     two pools alternate.  Bytes = read src + write codes + write scales."""
@@ -525,6 +576,11 @@ def all_configs(args, device):
     emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
     for page in (32, 64):
         emit(_decode_row(f"decode fp16 P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device, args, flush))
+    # Paged (chunked) prefill: K/V through the page table (page 16)
+    for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        emit(_paged_prefill_row(f"prefill paged {dn} causal L8192 P16", [8192], [8192], dt, device, args))
+        emit(_paged_prefill_row(f"prefill paged {dn} chunk 512 after 3584 B16", [4096] * 16, [512] * 16, dt,
+                                device, args))
     # KV write path (flashattn_tile/quant.py:84-142, paging.py:172-210): quantise the headline
     # pool; one-token append
     for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):

@@ -3,7 +3,8 @@
 Drop-in for the reference package's operator surface
 (``flashattn_tile/__init__.py:22-39``): importing registers the
 ``flashattn_tile::paged_decode`` / ``flashattn_tile::prefill_varlen`` custom
-ops (plus ``flashattn_tile::paged_decode_quant``), and the cache contract,
+ops (plus the extensions ``flashattn_tile::paged_decode_quant`` and
+``flashattn_tile::prefill_paged``), and the cache contract,
 quantisation helpers, kernel wrappers and backend keep their names.  Every op
 executes hand-written gfx950 HIP kernels (``csrc/``) through the C ABI of
 ``include/fat_abi.h``; there is no CPU fallback.  The reference's fp32 oracle
@@ -16,8 +17,9 @@ __version__ = "0.1.0"
 
 from . import ops as _ops  # noqa: F401  (registers the custom ops)
 from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
-from .kernels.prefill import prefill_attention
-from .ops import PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, paged_decode, paged_decode_quant, prefill_varlen
+from .kernels.prefill import paged_prefill_attention, prefill_attention
+from .ops import (PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, PREFILL_PAGED_OP, paged_decode,
+                  paged_decode_quant, prefill_paged, prefill_varlen)
 from .paging import PagedKVCache, allocate, append_tokens, gather_contiguous, gather_paged, validate_cache
 from .quant import QuantScales, dequantize_cache, kv_bytes_per_token, quantize_cache
 
@@ -26,9 +28,12 @@ __all__ = [
     "PAGED_DECODE_OP",
     "PREFILL_OP",
     "PAGED_DECODE_QUANT_OP",
+    "PREFILL_PAGED_OP",
     "paged_decode",
     "prefill_varlen",
     "paged_decode_quant",
+    "prefill_paged",
+    "paged_prefill_attention",
     "paged_decode_attention",
     "paged_decode_attention_fp8",
     "prefill_attention",

@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enum fat_dtype
 DT_F16 = 0
@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "fat_paged_decode",
     "fat_prefill_workspace_bytes",
     "fat_prefill_varlen",
+    "fat_prefill_paged",
     "fat_quantize_pages",
     "fat_append_kv",
 )
@@ -114,6 +115,43 @@ class PrefillArgs(ctypes.Structure):
         ("head_dim", _c_i32),
         ("max_seqlen_q", _c_i32),
         ("max_seqlen_k", _c_i32),
+        ("causal", _c_i32),
+        ("dtype", _c_i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class PrefillPagedArgs(ctypes.Structure):
+    """Mirror of ``fat_prefill_paged_args``."""
+
+    _fields_ = [
+        ("q", _c_vp),
+        ("k_cache", _c_vp),
+        ("v_cache", _c_vp),
+        ("page_table", _c_vp),
+        ("seq_lens", _c_vp),
+        ("cu_seqlens_q", _c_vp),
+        ("out", _c_vp),
+        ("q_stride_t", _c_i64),
+        ("q_stride_h", _c_i64),
+        ("k_stride_page", _c_i64),
+        ("k_stride_slot", _c_i64),
+        ("k_stride_head", _c_i64),
+        ("v_stride_page", _c_i64),
+        ("v_stride_slot", _c_i64),
+        ("v_stride_head", _c_i64),
+        ("page_table_stride", _c_i64),
+        ("out_stride_t", _c_i64),
+        ("out_stride_h", _c_i64),
+        ("batch", _c_i32),
+        ("total_q", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("page_size", _c_i32),
+        ("num_pages", _c_i32),
+        ("max_pages", _c_i32),
+        ("max_seqlen_q", _c_i32),
         ("causal", _c_i32),
         ("dtype", _c_i32),
         ("softmax_scale", ctypes.c_float),
@@ -222,6 +260,8 @@ def _load() -> None:
         lib.fat_prefill_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32]
         lib.fat_prefill_varlen.restype = ctypes.c_int
         lib.fat_prefill_varlen.argtypes = [ctypes.POINTER(PrefillArgs), _c_vp]
+        lib.fat_prefill_paged.restype = ctypes.c_int
+        lib.fat_prefill_paged.argtypes = [ctypes.POINTER(PrefillPagedArgs), _c_vp]
         lib.fat_quantize_pages.restype = ctypes.c_int
         lib.fat_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), _c_vp]
         lib.fat_append_kv.restype = ctypes.c_int
@@ -381,6 +421,50 @@ def prefill_varlen(
     a.softmax_scale = float(softmax_scale)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
+
+
+def prefill_paged(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    out: torch.Tensor,
+    page_size: int,
+    max_seqlen_q: int,
+    causal: bool,
+    softmax_scale: float,
+    stream: int | None = None,
+) -> None:
+    """Enqueue ``fat_prefill_paged`` for already-validated device tensors."""
+    a = PrefillPagedArgs()
+    a.q = _ptr(q)
+    a.k_cache = _ptr(k_cache)
+    a.v_cache = _ptr(v_cache)
+    a.page_table = _ptr(page_table)
+    a.seq_lens = _ptr(seq_lens)
+    a.cu_seqlens_q = _ptr(cu_seqlens_q)
+    a.out = _ptr(out)
+    a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1)
+    a.k_stride_page, a.k_stride_slot, a.k_stride_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.v_stride_page, a.v_stride_slot, a.v_stride_head = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.page_table_stride = page_table.stride(0)
+    a.out_stride_t, a.out_stride_h = out.stride(0), out.stride(1)
+    a.batch = cu_seqlens_q.shape[0] - 1
+    a.total_q = q.shape[0]
+    a.num_heads = q.shape[1]
+    a.num_kv_heads = k_cache.shape[2]
+    a.head_dim = q.shape[2]
+    a.page_size = int(page_size)
+    a.num_pages = k_cache.shape[0]
+    a.max_pages = page_table.shape[1]
+    a.max_seqlen_q = int(max_seqlen_q)
+    a.causal = 1 if causal else 0
+    a.dtype = dtype_code(q.dtype)
+    a.softmax_scale = float(softmax_scale)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    _check(lib().fat_prefill_paged(ctypes.byref(a), _c_vp(handle)), "fat_prefill_paged")
 
 
 def quantize_pages(src: torch.Tensor, dst: torch.Tensor, scale: torch.Tensor, stream: int | None = None) -> None:

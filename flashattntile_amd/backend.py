@@ -9,9 +9,12 @@ metadata fields and errors):
 * ``forward(query, kv_cache, attn_metadata)`` runs causal varlen prefill when
   ``attn_metadata.is_prefill`` and paged decode otherwise.
 
-An int8/fp8 :class:`PagedKVCache` is routed to the quantised decode kernel
-when ``attn_metadata.kv_scales`` carries its scales (an extension field; the
-reference backend had no quantised route).
+Two extension fields the reference backend lacks:
+* ``kv_scales``: an int8/fp8 :class:`PagedKVCache` is routed to the quantised
+  decode kernel when it carries the cache's scales;
+* ``paged_prefill``: prefill reads K/V from ``kv_cache`` through the page
+  table (chunked prefill; the chunk's own K/V already appended) instead of
+  from the packed ``k``/``v`` the reference requires (``backend.py:158-162``).
 """
 
 from __future__ import annotations
@@ -21,7 +24,7 @@ from dataclasses import dataclass
 import torch
 
 from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
-from .kernels.prefill import prefill_attention
+from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .paging import PagedKVCache, allocate
 
 KV_CACHE_NDIM = 4
@@ -44,6 +47,8 @@ class AttentionMetadata:
     softmax_scale: float | None = None
     # Scales of a quantised cache (QuantScales or {"k": ..., "v": ...}).
     kv_scales: object | None = None
+    # Prefill from the paged cache (chunk K/V already appended) instead of k/v.
+    paged_prefill: bool = False
 
 
 def get_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int,
@@ -110,6 +115,14 @@ class FlashAttnTileBackend:
         if query.shape[1] != self.num_heads:
             raise ValueError(f"query has {query.shape[1]} heads, backend expects {self.num_heads}")
 
+        if meta.is_prefill and meta.paged_prefill:
+            if meta.cu_seqlens_q is None:
+                raise ValueError("paged prefill routing requires cu_seqlens_q")
+            max_q = meta.max_seqlen_q
+            if max_q is None:
+                max_q = int((meta.cu_seqlens_q[1:] - meta.cu_seqlens_q[:-1]).max())
+            return paged_prefill_attention(query, cache, meta.cu_seqlens_q, int(max_q), causal=True,
+                                           softmax_scale=meta.softmax_scale)
         if meta.is_prefill:
             if meta.cu_seqlens_q is None or meta.cu_seqlens_k is None:
                 raise ValueError("prefill routing requires cu_seqlens_q and cu_seqlens_k")

@@ -27,7 +27,15 @@
 //   * exp is 2^(x * log2 e) on v_exp_f32;
 //   * the 1-D grid walks query blocks longest-first (causal balance) and
 //     assigns the query heads that share a KV head to the same XCD
-//     (workgroup id mod 8), so K/V blocks are reused from that XCD's L2.
+//     (workgroup id mod 8), so K/V blocks are reused from that XCD's L2;
+//   * paged instantiations (PG != 0: fat_prefill_paged, chunked prefill) read
+//     K/V through a page table from an NHD page pool instead of packed rows:
+//     key j of sequence b is slot j % P of page page_table[b, j / P], and
+//     kv_len is seq_lens[b].  Page ids are loaded one tile ahead, so the
+//     table lookup is off the load's critical path.  When a page holds at
+//     least the rows of one 16-byte-per-lane load (PG 2) the page id is
+//     wave-uniform and a load is a scalar base plus a constant lane offset;
+//     otherwise (PG 1) each lane forms its own 64-bit address.
 #include <stdlib.h>
 #include <string.h>
 
@@ -44,15 +52,106 @@ struct PrefillParams {
   const int32_t* cu_q;
   const int32_t* cu_k;
   uint8_t* out;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // element strides
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // element strides (k/v_st: slot stride when paged)
   int32_t B, H, Hkv, group, nqb;
   float scale_log2;
+  // Paged K/V (PAGED instantiations only).
+  const int32_t* pt;    // page table [B, max_pages]
+  const int32_t* lens;  // kv_len per sequence
+  int64_t pt_sb;        // page-table row stride
+  int64_t k_sp, v_sp;   // page strides (elements)
+  int32_t pshift;       // log2(page_size)
+  int32_t num_pages, max_pages;
 };
 
 constexpr int kBM = 128;
 constexpr int kBN = 64;
 // Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
 constexpr int kBufFlags = 0x00020000;
+
+// Rows of a K or V stream read through the page table.  A lane loads LOADS
+// 16-byte chunks per tile, at rows row0 + u * RPL (u < LOADS) of the tile and
+// byte column `col`.  The page ids a load needs are fetched by the previous
+// load of the same stream (tiles are loaded in increasing order), so the
+// table lookup latency hides behind a whole tile of compute.
+template <int LOADS, int RPL>
+struct PagedRows {
+  const uint8_t* base;  // cache + this KV head's offset
+  const int32_t* pt_row;
+  int64_t sp2;          // page stride, bytes
+  int64_t st2;          // slot stride, bytes
+  int pshift, pmask, kv_last, page_last, row0, col;
+  int pg[LOADS];
+
+  __device__ __forceinline__ int row_of(int tile, int u) const {
+    return min(tile * kBN + row0 + u * RPL, kv_last);
+  }
+  // Page ids of `tile` into pg (clamped into the pool: a bad table entry
+  // reads a wrong page, never outside the allocation).
+  __device__ __forceinline__ void fetch_ids(int tile) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) pg[u] = min(max(pt_row[row_of(tile, u) >> pshift], 0), page_last);
+  }
+  // The chunks of `tile` (its ids already in pg), then the ids of tile + 1.
+  __device__ __forceinline__ void load(int tile, u32x4 (&dst)[LOADS]) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int j = row_of(tile, u);
+      dst[u] = *reinterpret_cast<const u32x4*>(base + (int64_t)pg[u] * sp2 + (int64_t)(j & pmask) * st2 + col);
+    }
+    fetch_ids(tile + 1);
+  }
+};
+
+// The same streams when page_size >= RPL: the RPL rows of one load then lie
+// in one page, so its page id and the row base are wave-uniform (SGPRs) and
+// a lane adds only its constant offset -- no per-load vector address math.
+// Rows at or past kv_len (last tile only) read slots of the last page and
+// are zeroed before they reach LDS (mask_tail).
+template <int LOADS, int RPL>
+struct PagedRowsU {
+  const uint8_t* base;
+  const int32_t* pt_row;
+  int64_t sp2, st2;
+  int pshift, pmask, kv_len, last_idx, page_last, row0;
+  uint32_t lane_off;  // row0 * st2 + col
+  int pg[LOADS];      // page ids of the next tile (scalar registers)
+  int cur;            // tile whose chunks are in the registers
+
+  __device__ __forceinline__ int idx(int tile, int u) const {
+    return min((tile * kBN + u * RPL) >> pshift, last_idx);
+  }
+  // The table row is read-only for the kernel's lifetime, so its entries are
+  // read through the constant address space: uniform s_load_dword into SGPRs.
+  __device__ __forceinline__ void fetch_ids(int tile) {
+    const __attribute__((address_space(4))) int32_t* t =
+        (const __attribute__((address_space(4))) int32_t*)pt_row;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) pg[u] = t[idx(tile, u)];
+  }
+  // Each load is a buffer load whose descriptor base is the (uniform) row
+  // address and whose 32-bit lane offset is constant: no vector address math.
+  __device__ __forceinline__ void load(int tile, u32x4 (&dst)[LOADS]) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      const int page = min(max(pg[u], 0), page_last);
+      const int slot0 = (tile * kBN + u * RPL) & pmask;
+      const uint8_t* row_base = base + (int64_t)page * sp2 + (int64_t)slot0 * st2;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)row_base, (short)0, 0x7fffffff, kBufFlags);
+      dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, 0, 0));
+    }
+    cur = tile;
+    fetch_ids(tile + 1);
+  }
+  __device__ __forceinline__ void mask_tail(u32x4 (&dst)[LOADS]) const {
+    if (cur * kBN + kBN > kv_len) {  // wave-uniform
+#pragma unroll
+      for (int u = 0; u < LOADS; ++u)
+        if (cur * kBN + u * RPL + row0 >= kv_len) dst[u] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+};
 
 // A row's running max is only moved (and O rescaled) when a tile's max
 // exceeds it by more than this many log2 units; p = 2^(x - m) then stays
@@ -64,7 +163,7 @@ constexpr float kLazy = 8.0f;
 
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
-template <typename T, int D, bool CAUSAL, bool POS>
+template <typename T, int D, bool CAUSAL, bool POS, int PG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;        // MFMA k-steps of S^T over the head dim
@@ -94,8 +193,9 @@ void prefill_kernel(const PrefillParams p) {
 
   const int q_start = p.cu_q[b];
   const int q_len = p.cu_q[b + 1] - q_start;
-  const int k_start = p.cu_k[b];
-  const int kv_len = p.cu_k[b + 1] - k_start;
+  constexpr bool PAGED = PG != 0;
+  const int k_start = PAGED ? 0 : p.cu_k[b];
+  const int kv_len = PAGED ? min(max(p.lens[b], 0), p.max_pages << p.pshift) : p.cu_k[b + 1] - k_start;
   if (mb * kBM >= q_len) return;  // uniform over the workgroup
 
   const int tid = threadIdx.x;
@@ -136,6 +236,8 @@ void prefill_kernel(const PrefillParams p) {
   // K/V prefetch through buffer loads: the sequence's first row (this KV
   // head) is the scalar base and each lane keeps a 32-bit byte offset, so a
   // tile's addresses cost one add per load (no 64-bit vector arithmetic).
+  // (Measured: this beats moving the per-load row offset into the scalar
+  // descriptor base, whose extra SALU issue slots cost more than the add.)
   const uint8_t* kseq = p.k + 2 * ((int64_t)k_start * p.k_st + (int64_t)kvh * p.k_sh);
   const uint8_t* vseq = p.v + 2 * ((int64_t)k_start * p.v_st + (int64_t)kvh * p.v_sh);
   // Record sizes end at the last row's final byte; loads past them read 0.
@@ -152,21 +254,62 @@ void prefill_kernel(const PrefillParams p) {
   const int voff0 = (int)__umul24(tid / CPR, vst2) + 16 * (tid % CPR);
   constexpr int kRowsPerLoad = 256 / CPR;
   u32x4 kreg[LOADS], vreg[LOADS];
+  // Paged streams: the same lane -> (row, chunk) mapping.  PG 1: page id per
+  // lane and load; PG 2: page id per load (wave-uniform).
+  using Rows = std::conditional_t<PG == 2, PagedRowsU<LOADS, kRowsPerLoad>, PagedRows<LOADS, kRowsPerLoad>>;
+  Rows kpr, vpr;
+  if constexpr (PAGED) {
+    const int32_t* pt_row = p.pt + (int64_t)b * p.pt_sb;
+    kpr.base = p.k + 2 * (int64_t)kvh * p.k_sh;
+    vpr.base = p.v + 2 * (int64_t)kvh * p.v_sh;
+    kpr.sp2 = 2 * p.k_sp;
+    vpr.sp2 = 2 * p.v_sp;
+    kpr.st2 = 2 * p.k_st;
+    vpr.st2 = 2 * p.v_st;
+    kpr.pt_row = vpr.pt_row = pt_row;
+    kpr.pshift = vpr.pshift = p.pshift;
+    kpr.pmask = vpr.pmask = (1 << p.pshift) - 1;
+    kpr.page_last = vpr.page_last = p.num_pages - 1;
+    kpr.row0 = vpr.row0 = tid / CPR;
+    if constexpr (PG == 2) {
+      kpr.kv_len = vpr.kv_len = kv_len;
+      kpr.last_idx = vpr.last_idx = max(kv_len - 1, 0) >> p.pshift;
+      kpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.k_st + 16 * (tid % CPR));
+      vpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.v_st + 16 * (tid % CPR));
+      kpr.cur = vpr.cur = 0;
+    } else {
+      kpr.kv_last = vpr.kv_last = max(kv_len - 1, 0);
+      kpr.col = vpr.col = 16 * (tid % CPR);
+    }
+    if (n_tiles > 0) {
+      kpr.fetch_ids(0);
+      vpr.fetch_ids(0);
+    }
+  }
   auto gload_k = [&](int tile) {
-    const int base = koff0 + tile * kBN * kst2;
+    if constexpr (PAGED) {
+      kpr.load(tile, kreg);
+    } else {
+      const int base = koff0 + tile * kBN * kst2;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u)
-      kreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              krs, base + u * kRowsPerLoad * kst2, 0, 0));
+      for (int u = 0; u < LOADS; ++u)
+        kreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                krs, base + u * kRowsPerLoad * kst2, 0, 0));
+    }
   };
   auto gload_v = [&](int tile) {
-    const int base = voff0 + tile * kBN * vst2;
+    if constexpr (PAGED) {
+      vpr.load(tile, vreg);
+    } else {
+      const int base = voff0 + tile * kBN * vst2;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u)
-      vreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              vrs, base + u * kRowsPerLoad * vst2, 0, 0));
+      for (int u = 0; u < LOADS; ++u)
+        vreg[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                vrs, base + u * kRowsPerLoad * vst2, 0, 0));
+    }
   };
   auto lstore_k = [&](int buf) {
+    if constexpr (PG == 2) kpr.mask_tail(kreg);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
@@ -174,6 +317,7 @@ void prefill_kernel(const PrefillParams p) {
     }
   };
   auto lstore_v = [&](int buf) {
+    if constexpr (PG == 2) vpr.mask_tail(vreg);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
@@ -402,7 +546,7 @@ struct MfmaPhaseOrder {
 constexpr float kLazyPP = 15.0f;
 constexpr float kLazyPPSum = 32768.0f;  // 2^kLazyPP
 
-template <typename T, int D, bool CAUSAL, bool POS>
+template <typename T, int D, bool CAUSAL, bool POS, int PG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;
@@ -429,8 +573,9 @@ void prefill_pp_kernel(const PrefillParams p) {
 
   const int q_start = p.cu_q[b];
   const int q_len = p.cu_q[b + 1] - q_start;
-  const int k_start = p.cu_k[b];
-  const int kv_len = p.cu_k[b + 1] - k_start;
+  constexpr bool PAGED = PG != 0;
+  const int k_start = PAGED ? 0 : p.cu_k[b];
+  const int kv_len = PAGED ? min(max(p.lens[b], 0), p.max_pages << p.pshift) : p.cu_k[b + 1] - k_start;
   if (mb * kPBM >= q_len) return;  // uniform over the workgroup
 
   const int tid = threadIdx.x;
@@ -480,14 +625,42 @@ void prefill_pp_kernel(const PrefillParams p) {
   const int lds_buf = grp ? kBN * V_RS : kBN * K_RS;
   const int lds_off = (gt / CPR) * lds_rs + 8 * (gt % CPR);
   u32x4 stage[LOADS];
+  // PAGED only: this group's K or V stream (PG 1 per-lane page ids, PG 2
+  // wave-uniform ones).
+  std::conditional_t<PG == 2, PagedRowsU<LOADS, kRowsPerLoad>, PagedRows<LOADS, kRowsPerLoad>> pr;
+  if constexpr (PAGED) {
+    pr.base = (grp ? p.v : p.k) + 2 * (int64_t)kvh * sh;
+    pr.pt_row = p.pt + (int64_t)b * p.pt_sb;
+    pr.sp2 = 2 * (grp ? p.v_sp : p.k_sp);
+    pr.st2 = st2;
+    pr.pshift = p.pshift;
+    pr.pmask = (1 << p.pshift) - 1;
+    pr.page_last = p.num_pages - 1;
+    pr.row0 = gt / CPR;
+    if constexpr (PG == 2) {
+      pr.kv_len = kv_len;
+      pr.last_idx = max(kv_len - 1, 0) >> p.pshift;
+      pr.lane_off = (uint32_t)((gt / CPR) * st2 + 16 * (gt % CPR));
+      pr.cur = 0;
+    } else {
+      pr.kv_last = max(kv_len - 1, 0);
+      pr.col = 16 * (gt % CPR);
+    }
+    if (n_tiles > 0) pr.fetch_ids(0);
+  }
   auto gload = [&](int tile) {
-    const int base = off0 + tile * kBN * st2;
+    if constexpr (PAGED) {
+      pr.load(tile, stage);
+    } else {
+      const int base = off0 + tile * kBN * st2;
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u)
-      stage[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rs, base + u * kRowsPerLoad * st2, 0, 0));
+      for (int u = 0; u < LOADS; ++u)
+        stage[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rs, base + u * kRowsPerLoad * st2, 0, 0));
+    }
   };
   auto lstore = [&](int buf) {
+    if constexpr (PG == 2) pr.mask_tail(stage);
     uint16_t* dst = lds0 + buf * lds_buf + lds_off;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u)
@@ -695,35 +868,66 @@ void prefill_pp_kernel(const PrefillParams p) {
 // ===========================================================================
 namespace {
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, int PG>
 void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
   if (pos) {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true>), grid, dim3(256), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true, PG>), grid, dim3(256), 0, stream, prm);
   } else {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false>), grid, dim3(256), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false, PG>), grid, dim3(256), 0, stream, prm);
   }
 }
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, int PG>
 void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
   if (pos) {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true>), grid, dim3(512), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true, PG>), grid, dim3(512), 0, stream, prm);
   } else {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false>), grid, dim3(512), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false, PG>), grid, dim3(512), 0, stream, prm);
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int PG>
 int launch_prefill_t(const fat::PrefillParams& prm, bool causal, bool pingpong, dim3 grid, hipStream_t stream) {
   const bool pos = prm.scale_log2 > 0.f;
   if (pingpong) {
-    if (causal) launch_prefill_pp_c<T, D, true>(prm, pos, grid, stream);
-    else launch_prefill_pp_c<T, D, false>(prm, pos, grid, stream);
+    if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
+    else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
     return fat_host::launch_status("prefill_pp_kernel");
   }
-  if (causal) launch_prefill_c<T, D, true>(prm, pos, grid, stream);
-  else launch_prefill_c<T, D, false>(prm, pos, grid, stream);
+  if (causal) launch_prefill_c<T, D, true, PG>(prm, pos, grid, stream);
+  else launch_prefill_c<T, D, false, PG>(prm, pos, grid, stream);
   return fat_host::launch_status("prefill_kernel");
+}
+
+// Kernel choice and grid shared by fat_prefill_varlen and fat_prefill_paged.
+// The 8-wave ping-pong kernel needs a grid of at least FAT_PF_PP_MIN
+// 256-row workgroups to fill the chip; smaller problems use the 4-wave,
+// 128-row kernel (twice the workgroups).  FAT_PREFILL_KERNEL=pingpong|4wave
+// overrides the choice (tests exercise both kernels on every shape).
+template <int PG>
+int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int dtype, int D, bool causal, float softmax_scale,
+                   const char* who, hipStream_t stream) {
+  const int64_t nqb_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM;
+  bool pingpong = nqb_pp * prm.B * prm.H >= FAT_PF_PP_MIN;
+  if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
+    if (!strcmp(force, "pingpong")) pingpong = true;
+    else if (!strcmp(force, "4wave")) pingpong = false;
+  }
+  const int bm = pingpong ? fat::kPBM : fat::kBM;
+  prm.nqb = (max_seqlen_q + bm - 1) / bm;
+  prm.scale_log2 = softmax_scale * fat::kLog2e;
+  const int64_t n = (int64_t)prm.nqb * prm.B * prm.H;
+  if (n > 0x7fffffff) {
+    fat_host::set_error("%s: too many query blocks (%lld)", who, (long long)n);
+    return FAT_E_UNSUPPORTED;
+  }
+  const dim3 grid((unsigned)n);
+  if (dtype == FAT_DTYPE_F16) {
+    return D == 128 ? launch_prefill_t<fat::F16, 128, PG>(prm, causal, pingpong, grid, stream)
+                    : launch_prefill_t<fat::F16, 64, PG>(prm, causal, pingpong, grid, stream);
+  }
+  return D == 128 ? launch_prefill_t<fat::BF16, 128, PG>(prm, causal, pingpong, grid, stream)
+                  : launch_prefill_t<fat::BF16, 64, PG>(prm, causal, pingpong, grid, stream);
 }
 
 }  // namespace
@@ -805,32 +1009,102 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = a->num_heads / a->num_kv_heads;
-  // The 8-wave ping-pong kernel needs a grid of at least FAT_PF_PP_MIN
-  // 256-row workgroups to fill the chip; smaller problems use the 4-wave,
-  // 128-row kernel (twice the workgroups).
-  const int64_t nqb_pp = (a->max_seqlen_q + fat::kPBM - 1) / fat::kPBM;
-  bool pingpong = nqb_pp * a->batch * a->num_heads >= FAT_PF_PP_MIN;
-  // FAT_PREFILL_KERNEL=pingpong|4wave overrides the choice (tests exercise
-  // both kernels on every shape); anything else keeps the automatic one.
-  if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
-    if (!strcmp(force, "pingpong")) pingpong = true;
-    else if (!strcmp(force, "4wave")) pingpong = false;
+  return launch_prefill<0>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
+                               "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
+}
+
+extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_ptr) {
+  fat_host::clear_error();
+  if (!a) {
+    fat_host::set_error("fat_prefill_paged: args is NULL");
+    return FAT_E_INVALID;
   }
-  const int bm = pingpong ? fat::kPBM : fat::kBM;
-  prm.nqb = (a->max_seqlen_q + bm - 1) / bm;
-  prm.scale_log2 = a->softmax_scale * fat::kLog2e;
-  const int64_t n = (int64_t)prm.nqb * a->batch * a->num_heads;
-  if (n > 0x7fffffff) {
-    fat_host::set_error("fat_prefill_varlen: too many query blocks (%lld)", (long long)n);
+  if (!a->q || !a->k_cache || !a->v_cache || !a->page_table || !a->seq_lens || !a->cu_seqlens_q || !a->out) {
+    fat_host::set_error("fat_prefill_paged: a required pointer is NULL");
+    return FAT_E_INVALID;
+  }
+  if (a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->total_q < 0 || a->num_pages <= 0 ||
+      a->max_pages <= 0) {
+    fat_host::set_error("fat_prefill_paged: batch, head counts, num_pages and max_pages must be positive");
+    return FAT_E_INVALID;
+  }
+  if (a->num_heads % a->num_kv_heads != 0) {
+    fat_host::set_error("fat_prefill_paged: num_heads %d must be divisible by num_kv_heads %d", a->num_heads,
+                        a->num_kv_heads);
+    return FAT_E_INVALID;
+  }
+  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16) {
+    fat_host::set_error("fat_prefill_paged: dtype must be fp16 or bf16");
     return FAT_E_UNSUPPORTED;
   }
-  const dim3 grid((unsigned)n);
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  const bool causal = a->causal != 0;
-  if (a->dtype == FAT_DTYPE_F16) {
-    return D == 128 ? launch_prefill_t<fat::F16, 128>(prm, causal, pingpong, grid, stream)
-                    : launch_prefill_t<fat::F16, 64>(prm, causal, pingpong, grid, stream);
+  const int D = a->head_dim;
+  if (D != 64 && D != 128) {
+    fat_host::set_error("fat_prefill_paged: head_dim %d unsupported (64 or 128)", D);
+    return FAT_E_UNSUPPORTED;
   }
-  return D == 128 ? launch_prefill_t<fat::BF16, 128>(prm, causal, pingpong, grid, stream)
-                  : launch_prefill_t<fat::BF16, 64>(prm, causal, pingpong, grid, stream);
+  const int P = a->page_size;
+  if (P <= 0 || P > 4096 || (P & (P - 1)) != 0) {
+    fat_host::set_error("fat_prefill_paged: page_size %d must be a power of two in [1, 4096]", P);
+    return FAT_E_UNSUPPORTED;
+  }
+  if ((int64_t)a->max_pages * P > 0x7fffffffLL) {
+    fat_host::set_error("fat_prefill_paged: max_pages * page_size overflows int32 positions");
+    return FAT_E_INVALID;
+  }
+  if (a->max_seqlen_q < 0) {
+    fat_host::set_error("fat_prefill_paged: max_seqlen_q must be non-negative");
+    return FAT_E_INVALID;
+  }
+  const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
+                            (uintptr_t)(2 * a->q_stride_t) | (uintptr_t)(2 * a->q_stride_h) |
+                            (uintptr_t)(2 * a->k_stride_page) | (uintptr_t)(2 * a->k_stride_slot) |
+                            (uintptr_t)(2 * a->k_stride_head) | (uintptr_t)(2 * a->v_stride_page) |
+                            (uintptr_t)(2 * a->v_stride_slot) | (uintptr_t)(2 * a->v_stride_head);
+  const uintptr_t align8 = (uintptr_t)a->out | (uintptr_t)(2 * a->out_stride_t) | (uintptr_t)(2 * a->out_stride_h);
+  if ((align16 & 15) || (align8 & 7)) {
+    fat_host::set_error("fat_prefill_paged: q and cache rows must be 16-byte aligned and out rows 8-byte aligned");
+    return FAT_E_INVALID;
+  }
+  if (a->max_seqlen_q == 0 || a->total_q == 0) return FAT_OK;  // nothing to compute
+
+  fat::PrefillParams prm{};
+  prm.q = static_cast<const uint8_t*>(a->q);
+  prm.k = static_cast<const uint8_t*>(a->k_cache);
+  prm.v = static_cast<const uint8_t*>(a->v_cache);
+  prm.cu_q = a->cu_seqlens_q;
+  prm.cu_k = nullptr;
+  prm.out = static_cast<uint8_t*>(a->out);
+  prm.q_st = a->q_stride_t;
+  prm.q_sh = a->q_stride_h;
+  prm.k_st = a->k_stride_slot;
+  prm.k_sh = a->k_stride_head;
+  prm.v_st = a->v_stride_slot;
+  prm.v_sh = a->v_stride_head;
+  prm.o_st = a->out_stride_t;
+  prm.o_sh = a->out_stride_h;
+  prm.B = a->batch;
+  prm.H = a->num_heads;
+  prm.Hkv = a->num_kv_heads;
+  prm.group = a->num_heads / a->num_kv_heads;
+  prm.pt = a->page_table;
+  prm.lens = a->seq_lens;
+  prm.pt_sb = a->page_table_stride;
+  prm.k_sp = a->k_stride_page;
+  prm.v_sp = a->v_stride_page;
+  prm.pshift = __builtin_ctz((unsigned)P);
+  prm.num_pages = a->num_pages;
+  prm.max_pages = a->max_pages;
+  // One load covers 256 / (D / 8) rows (16 at D128, 32 at D64): with pages at
+  // least that long its rows share a page and the page id is wave-uniform.
+  // FAT_PREFILL_PAGED_ROWS=lane forces the per-lane variant (tests).
+  bool uniform = P >= 256 / (D / 8);
+  if (const char* force = getenv("FAT_PREFILL_PAGED_ROWS")) {
+    if (!strcmp(force, "lane")) uniform = false;
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (uniform)
+    return launch_prefill<2>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
+                             "fat_prefill_paged", stream);
+  return launch_prefill<1>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
+                           "fat_prefill_paged", stream);
 }

@@ -7,6 +7,11 @@ accumulation; the Triton tile knobs (BLOCK_M/BLOCK_N/num_warps/num_stages)
 are validated as in the reference but the gfx950 kernel uses its own fixed
 tiling.  There is no CPU fallback: non-ROCm tensors or a dtype other than
 fp16/bf16 raise.
+
+``paged_prefill_attention`` is the paged (chunked) form the reference lacks:
+the queries of each sequence attend to that sequence's keys in a
+:class:`PagedKVCache` (its own new tokens appended first), read through the
+page table by the same gfx950 kernels.
 """
 
 from __future__ import annotations
@@ -14,8 +19,10 @@ from __future__ import annotations
 import torch
 
 from .. import _hip
+from ..paging import PagedKVCache, _check_layout
 
-__all__ = ["DEFAULT_CONFIG", "prefill_attention", "prefill_launch"]
+__all__ = ["DEFAULT_CONFIG", "prefill_attention", "prefill_launch", "paged_prefill_attention",
+           "paged_prefill_launch"]
 
 DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3}
 
@@ -163,3 +170,107 @@ def prefill_attention(
     v = v if v.stride(-1) == 1 else v.contiguous()
     return prefill_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
                           bool(causal), scale)
+
+
+def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
+    """Shape/dtype checks plus the device-side ones (cu_seqlens_q monotone
+    and ending at q.shape[0]; lengths within the table; used pages inside the
+    pool; kv_len >= q_len when causal) in one synchronisation.  The messages
+    are those of ``prefill.py:194-233`` and ``paging.py:84-130``.  Returns the
+    longest query sequence."""
+    if not isinstance(cache, PagedKVCache):
+        raise TypeError("cache must be a PagedKVCache")
+    _check_layout(cache)
+    if q.dim() != 3:
+        raise ValueError("q must be 3-D [tokens, heads, head_dim]")
+    if q.shape[-1] != cache.head_dim:
+        raise ValueError(f"q head_dim {q.shape[-1]} != cache head_dim {cache.head_dim}")
+    if q.dtype != cache.k_cache.dtype:
+        raise ValueError(f"q dtype {q.dtype} != cache dtype {cache.k_cache.dtype}")
+    if q.shape[1] % cache.num_kv_heads != 0:
+        raise ValueError(f"num_heads ({q.shape[1]}) must be divisible by num_kv_heads ({cache.num_kv_heads})")
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_q.dtype != torch.int32:
+        raise ValueError("cu_seqlens_q must be a 1-D int32 tensor")
+    if cu_seqlens_q.shape[0] != cache.batch_size + 1:
+        raise ValueError(f"cu_seqlens_q must have batch + 1 = {cache.batch_size + 1} entries, "
+                         f"got {cu_seqlens_q.shape[0]}")
+    dev = q.device
+    if any(t.device != dev for t in (cache.k_cache, cache.page_table, cache.seq_lens, cu_seqlens_q)):
+        raise ValueError("q, the cache, its page table, seq_lens and cu_seqlens_q must live on one device")
+    cq = cu_seqlens_q.to(torch.int64)
+    lq = cq[1:] - cq[:-1]
+    sl = cache.seq_lens.to(torch.int64)
+    P = cache.page_size
+    need = torch.div(sl.max() + (P - 1), P, rounding_mode="floor")
+    pt = cache.page_table
+    used = (torch.arange(pt.shape[1], device=dev) < need).unsqueeze(0).expand_as(pt)
+    big, small = torch.iinfo(torch.int32).max, torch.iinfo(torch.int32).min
+    lo = torch.where(used, pt, torch.full_like(pt, big)).min().to(torch.int64) if pt.numel() else sl.max() * 0
+    hi = torch.where(used, pt, torch.full_like(pt, small)).max().to(torch.int64) if pt.numel() else sl.max() * 0
+    stats = torch.stack([
+        cq[0], cq[-1], (lq < 0).any().to(torch.int64), lq.max(), (sl < lq).any().to(torch.int64),
+        sl.min(), sl.max(), lo, hi,
+    ]).cpu().tolist()
+    q0, q_end, q_dec, max_q, short_kv, min_len, max_len, lo, hi = (int(x) for x in stats)
+    if q0 != 0:
+        raise ValueError("cu_seqlens must start at 0")
+    if q_end != q.shape[0]:
+        raise ValueError("cu_seqlens_q[-1] must equal q.shape[0]")
+    if q_dec:
+        raise ValueError("cu_seqlens_q must be non-decreasing")
+    if min_len < 0:
+        raise AssertionError("seq_lens must be non-negative")
+    if max_len > cache.capacity:
+        raise AssertionError(f"seq_len {max_len} exceeds page-table capacity {cache.capacity}")
+    if max_len > 0 and lo != big:
+        if lo < 0:
+            raise AssertionError("page_table contains a negative page id")
+        if hi >= cache.num_pages:
+            raise AssertionError(f"page_table references page {hi} but cache has {cache.num_pages} pages")
+    if causal and short_kv:
+        raise ValueError("causal bottom-right alignment requires kv_len >= q_len per sequence")
+    return max_q
+
+
+def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: torch.Tensor, max_seqlen_q: int,
+                         causal: bool, softmax_scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Enqueue ``fat_prefill_paged`` without validation or synchronisation."""
+    if q.stride(-1) != 1 or cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
+        raise ValueError("q and the cache need a contiguous head_dim axis")
+    if out is None:
+        out = torch.empty_like(q)
+    pt = cache.page_table if cache.page_table.stride(-1) == 1 else cache.page_table.contiguous()
+    sl = cache.seq_lens if cache.seq_lens.is_contiguous() else cache.seq_lens.contiguous()
+    _hip.prefill_paged(q, cache.k_cache, cache.v_cache, pt, sl, cu_seqlens_q, out, cache.page_size,
+                       int(max_seqlen_q), bool(causal), float(softmax_scale))
+    return out
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    cu_seqlens_q: torch.Tensor,
+    max_seqlen_q: int,
+    causal: bool = True,
+    softmax_scale: float | None = None,
+) -> torch.Tensor:
+    """Paged (chunked) prefill: ``q`` ``[total_q, num_heads, head_dim]`` packed
+    by ``cu_seqlens_q`` (int32 ``[B + 1]``) attends, per sequence b, to keys
+    ``0 .. seq_lens[b] - 1`` of ``cache`` (which already holds the chunk's
+    own K/V).  Causal masking is bottom-right aligned, as in
+    :func:`prefill_attention`, so query i of a q_len-token chunk sees keys
+    ``j <= i + seq_lens[b] - q_len``.  Returns ``q``'s shape and dtype.
+    """
+    longest_q = _validate_paged(q, cache, cu_seqlens_q, causal)
+    if max_seqlen_q <= 0:
+        raise ValueError(f"max_seqlen_q must be positive, got {max_seqlen_q}")
+    if max_seqlen_q < longest_q:
+        raise ValueError(f"max_seqlen_q {max_seqlen_q} is smaller than the longest query sequence {longest_q}")
+    if not q.is_cuda:
+        raise RuntimeError("paged_prefill_attention: inputs must be ROCm device tensors; this build runs the "
+                           "gfx950 HIP kernel only (no CPU or reference fallback)")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"paged_prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    return paged_prefill_launch(q, cache, cu_seqlens_q, int(max_seqlen_q), bool(causal), scale)

@@ -11,12 +11,17 @@ Same namespace, names and schemas as ``flashattn_tile/ops.py:35-122``:
     SymInt max_seqlen_q, SymInt max_seqlen_k, bool causal,
     float softmax_scale) -> Tensor``
 
-plus one extension the reference lacks (its quantised decode had no op):
+plus two extensions the reference lacks (its quantised decode had no op,
+and its prefill needs packed K/V):
 
 ``flashattn_tile::paged_decode_quant``
     ``(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,
     Tensor v_scale, Tensor page_table, Tensor seq_lens, SymInt page_size,
     float softmax_scale, SymInt split_k) -> Tensor``
+``flashattn_tile::prefill_paged``
+    ``(Tensor q, Tensor k_cache, Tensor v_cache, Tensor page_table,
+    Tensor seq_lens, Tensor cu_seqlens_q, SymInt max_seqlen_q,
+    SymInt page_size, bool causal, float softmax_scale) -> Tensor``
 
 The real implementations call the gfx950 HIP kernels through the C ABI; the
 fake implementations touch metadata only, so ``torch.compile(fullgraph=True)``
@@ -28,22 +33,25 @@ from __future__ import annotations
 import torch
 
 from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
-from .kernels.prefill import prefill_attention
+from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .paging import PagedKVCache
 
 __all__ = [
     "paged_decode",
     "prefill_varlen",
     "paged_decode_quant",
+    "prefill_paged",
     "ops_available",
     "PAGED_DECODE_OP",
     "PREFILL_OP",
     "PAGED_DECODE_QUANT_OP",
+    "PREFILL_PAGED_OP",
 ]
 
 PAGED_DECODE_OP = "flashattn_tile::paged_decode"
 PREFILL_OP = "flashattn_tile::prefill_varlen"
 PAGED_DECODE_QUANT_OP = "flashattn_tile::paged_decode_quant"
+PREFILL_PAGED_OP = "flashattn_tile::prefill_paged"
 
 
 @torch.library.custom_op(PAGED_DECODE_OP, mutates_args=())
@@ -129,7 +137,38 @@ def _paged_decode_quant_fake(q, k_cache, v_cache, k_scale, v_scale, page_table, 
     return q.new_empty(q.shape)
 
 
+@torch.library.custom_op(PREFILL_PAGED_OP, mutates_args=())
+def prefill_paged(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    max_seqlen_q: int,
+    page_size: int,
+    causal: bool,
+    softmax_scale: float,
+) -> torch.Tensor:
+    """Paged (chunked) prefill: packed queries against each sequence's
+    ``seq_lens[b]`` keys in the paged cache (extension of ``ops.py:76-99``)."""
+    cache = PagedKVCache(k_cache=k_cache, v_cache=v_cache, page_table=page_table,
+                         seq_lens=seq_lens, page_size=int(page_size))
+    return paged_prefill_attention(q, cache, cu_seqlens_q, int(max_seqlen_q), causal=bool(causal),
+                                   softmax_scale=softmax_scale)
+
+
+@prefill_paged.register_fake
+def _prefill_paged_fake(q, k_cache, v_cache, page_table, seq_lens, cu_seqlens_q, max_seqlen_q, page_size, causal,
+                        softmax_scale):
+    torch._check(q.dim() == 3, lambda: f"q must be 3-D, got {q.dim()}")
+    torch._check(cu_seqlens_q.shape[0] == seq_lens.shape[0] + 1, lambda: "cu_seqlens_q must have batch + 1 entries")
+    torch._check(q.shape[2] == k_cache.shape[3], lambda: "q head_dim must match cache")
+    torch._check(q.shape[1] % k_cache.shape[2] == 0, lambda: "heads must be divisible by KV heads")
+    return q.new_empty(q.shape)
+
+
 def ops_available() -> bool:
     """True when the custom ops are registered in this process."""
     return all(hasattr(torch.ops.flashattn_tile, name)
-               for name in ("paged_decode", "prefill_varlen", "paged_decode_quant"))
+               for name in ("paged_decode", "prefill_varlen", "paged_decode_quant", "prefill_paged"))

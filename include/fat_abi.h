@@ -22,6 +22,11 @@
  *                          (paged_decode_attention_fp8: _decode_paged_quant_kernel)
  *   fat_prefill_varlen     flashattn_tile/kernels/prefill.py:236-326
  *                          (prefill_attention: _fwd_varlen_kernel)
+ *   fat_prefill_paged      no reference counterpart: the paged (chunked)
+ *                          prefill that flashattn_tile/backend.py:158-162
+ *                          lacks (it requires packed K/V); semantics of
+ *                          flashattn_tile/kernels/prefill.py:35-138 with K/V
+ *                          read through the page table
  *   fat_quantize_pages     flashattn_tile/quant.py:84-142
  *                          (quantize_kv_pages, one of K or V per call)
  *   fat_append_kv          flashattn_tile/paging.py:172-210
@@ -38,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 3
+#define FAT_ABI_VERSION 4
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -155,6 +160,50 @@ typedef struct fat_prefill_args {
 } fat_prefill_args;
 
 /*
+ * Paged (chunked) prefill: the packed queries of each sequence attend to the
+ * sequence's keys in a paged K/V cache.
+ *   q   [total_q, num_heads, head_dim]                     dtype
+ *   k_cache, v_cache [num_pages, page_size, num_kv_heads, head_dim]  dtype
+ *   page_table int32 [batch, max_pages], seq_lens int32 [batch]: key j of
+ *   sequence b is slot j % page_size of page page_table[b, j / page_size],
+ *   for j < kv_len = seq_lens[b] (the chunk's own keys included).
+ *   cu_seqlens_q int32 [batch + 1], starting at 0, non-decreasing;
+ *   kv_len >= q_len per sequence when causal.
+ *   out [total_q, num_heads, head_dim]                     dtype
+ * Causal masking is bottom-right aligned, as fat_prefill_varlen: query i of
+ * a sequence sees key j iff j <= i + (kv_len - q_len).  page_size must be a
+ * power of two.  Page ids are clamped to [0, num_pages) and kv_len to
+ * max_pages * page_size on the device, so a bad table gives a wrong answer,
+ * never an out-of-bounds read.  No workspace.
+ */
+typedef struct fat_prefill_paged_args {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* page_table;
+  const int32_t* seq_lens;
+  const int32_t* cu_seqlens_q;
+  void* out;
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_page, k_stride_slot, k_stride_head;
+  int64_t v_stride_page, v_stride_slot, v_stride_head;
+  int64_t page_table_stride;
+  int64_t out_stride_t, out_stride_h;
+  int32_t batch;
+  int32_t total_q;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t num_pages;
+  int32_t max_pages;
+  int32_t max_seqlen_q;
+  int32_t causal;
+  int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
+  float softmax_scale;
+} fat_prefill_paged_args;
+
+/*
  * Per-(page, KV head) quantisation of a paged cache tensor.
  *   src   [num_pages, page_size, num_kv_heads, head_dim]  src_dtype
  *   dst   same shape                                       dst_dtype
@@ -249,6 +298,12 @@ size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
 /* Enqueue varlen prefill on `stream`.
  * Replaces flashattn_tile/kernels/prefill.py:236-326 (see file header). */
 int fat_prefill_varlen(const fat_prefill_args* args, void* stream);
+
+/* Enqueue paged (chunked) prefill on `stream`.  Extends
+ * flashattn_tile/kernels/prefill.py:236-326 to K/V read through the page
+ * table (the reference has no counterpart; its backend needs packed K/V,
+ * flashattn_tile/backend.py:158-162). */
+int fat_prefill_paged(const fat_prefill_paged_args* args, void* stream);
 
 /* Enqueue the quantisation of one paged K or V tensor on `stream`.
  * Replaces flashattn_tile/quant.py:84-142 (quantize_kv_pages). */

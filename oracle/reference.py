@@ -25,6 +25,14 @@ Functions and what pins them (tests/test_oracle.py, tests/test_quant.py):
     with varlen on the contiguous gather.
 ``ref_attention_dense``  (reference.py:197-219)
     token-major transpose wrapper; pinned against per-batch varlen.
+``ref_attention_paged_prefill``  (no reference counterpart: the chunked
+    prefill the reference's backend lacks, backend.py:158-162)
+    gathers each sequence's seq_lens[b] keys through the table (as
+    reference.py:177-186), then varlen with the packed queries.  Pinned by
+    equality with ref_attention_paged when every chunk is one query, with
+    ref_attention_varlen when the pool holds the packed K/V in order, by
+    page-table permutation invariance, and by the chunking identity: a causal
+    sequence prefilled as two chunks gives the rows of the one-shot prefill.
 ``lse_partials`` / ``lse_merge``  (docs/kernel_design.md:84-94,
     kernels/decode.py:316-356)
     split-K restatement used to check the merge algebra: merging any
@@ -182,6 +190,25 @@ def ref_attention_paged(q, k_cache, v_cache, page_table, seq_lens, causal: bool 
         cu_k.append(cu_k[-1] + n)
     cu_q = list(range(len(lens) + 1))
     return ref_attention_varlen(q.detach().cpu(), k_packed, v_packed, cu_q, cu_k, causal=causal,
+                                softmax_scale=softmax_scale, return_fp32=return_fp32)
+
+
+def ref_attention_paged_prefill(q, k_cache, v_cache, page_table, seq_lens, cu_seqlens_q, causal: bool = True,
+                                softmax_scale: float | None = None, return_fp32: bool = False) -> torch.Tensor:
+    """Packed queries ``q [total_q, H, D]`` (offsets ``cu_seqlens_q``) against
+    the first ``seq_lens[b]`` keys of each sequence in a paged cache."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be [tokens, heads, head_dim], got {tuple(q.shape)}")
+    if not k_cache.is_floating_point():
+        raise ValueError(f"reference attention needs a dequantized float cache, got {k_cache.dtype}; "
+                         "dequantize it first")
+    ks, vs = gather_pages(k_cache, v_cache, page_table, seq_lens)
+    cu_k = [0]
+    for t in ks:
+        cu_k.append(cu_k[-1] + t.shape[0])
+    k_packed = torch.cat(ks, dim=0)
+    v_packed = torch.cat(vs, dim=0)
+    return ref_attention_varlen(q.detach().cpu(), k_packed, v_packed, cu_seqlens_q, cu_k, causal=causal,
                                 softmax_scale=softmax_scale, return_fp32=return_fp32)
 
 

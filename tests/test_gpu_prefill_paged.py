@@ -1,0 +1,183 @@
+"""GPU parity of the paged (chunked) prefill, ``fat_prefill_paged``.
+
+Each sequence's queries (a chunk of q_len tokens) attend to the first
+seq_lens[b] keys of a paged cache whose pages are scattered by a seeded
+permutation and whose slots past each sequence end are poisoned (K = 30,
+V = 500).  The oracle is ``ref_attention_paged_prefill`` (gather through the
+table, then the fp32 varlen restatement of flashattn_tile/reference.py); the
+tolerance is the north star's 2e-3 on the kernel's result before its final
+rounding (tests/_parity.py).  Every shape runs on both prefill kernels.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from _parity import assert_parity, make_paged
+from flashattntile_amd import PagedKVCache
+from flashattntile_amd.kernels.prefill import paged_prefill_attention, prefill_attention
+from flashattntile_amd.paging import gather_contiguous
+from oracle.reference import ref_attention_paged_prefill
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(params=["auto", "pingpong", "4wave"])
+def kernel(request, monkeypatch):
+    monkeypatch.setenv("FAT_PREFILL_KERNEL", request.param)
+    return request.param
+
+
+def _case(lens_k, lens_q, h, hk, d, P, dtype, seed):
+    k, v, pt, sl = make_paged(lens_k, hk, d, P, dtype, seed=seed, device=DEV)
+    g = torch.Generator().manual_seed(seed + 100)
+    q = torch.randn(sum(lens_q), h, d, generator=g).to(dtype).to(DEV)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens_q), 0).tolist(), dtype=torch.int32, device=DEV)
+    return q, PagedKVCache(k, v, pt, sl, P), cu
+
+
+def _ref32(q, cache, cu, causal, scale=None):
+    return ref_attention_paged_prefill(q.cpu(), cache.k_cache.cpu(), cache.v_cache.cpu(), cache.page_table.cpu(),
+                                       cache.seq_lens.cpu(), cu.cpu(), causal=causal, softmax_scale=scale,
+                                       return_fp32=True)
+
+
+# chunks: (kv_len, q_len) per sequence -- a whole prompt, a chunk after a
+# prefix, single-token chunks (multi-sequence decode), a chunk crossing pages
+CHUNKS = [(1000, 1000), (300, 77), (129, 1), (64, 64), (517, 200), (5, 3)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("h,hk", [(8, 8), (8, 2), (32, 8), (8, 1)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
+    label = f"paged prefill {kernel} {dtype} D{d} H{h}/{hk} causal={causal}"
+    print(label, flush=True)
+    lens_k = [c[0] for c in CHUNKS]
+    lens_q = [c[1] for c in CHUNKS]
+    q, cache, cu = _case(lens_k, lens_q, h, hk, d, 16, dtype, seed=d + h + hk)
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=causal)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and out.dtype == dtype
+    assert_parity(out, _ref32(q, cache, cu, causal), label=label)
+
+
+@pytest.mark.parametrize("P", [1, 4, 16, 32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_prefill_page_sizes(P, dtype, kernel):
+    label = f"paged prefill {kernel} P{P} {dtype}"
+    print(label, flush=True)
+    lens_k, lens_q = [333, 64, 1, 200], [100, 64, 1, 7]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, P, dtype, seed=P)
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, softmax_scale=0.06)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache, cu, True, scale=0.06), label=label)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_prefill_equals_packed_prefill(dtype, kernel):
+    """The same keys, paged or packed: both prefill kernels agree bit for bit
+    (the paged path changes only where K/V rows are read from)."""
+    lens = [700, 129, 1, 64]
+    q, cache, cu = _case(lens, lens, 16, 4, 128, 16, dtype, seed=5)
+    k, v = gather_contiguous(cache)
+    pk = torch.cat([k[b, :n] for b, n in enumerate(lens)])
+    pv = torch.cat([v[b, :n] for b, n in enumerate(lens)])
+    out_paged = paged_prefill_attention(q, cache, cu, max(lens), causal=True)
+    out_packed = prefill_attention(q, pk, pv, cu, cu, max(lens), max(lens), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_paged, out_packed)
+
+
+def test_paged_prefill_chunked_equals_one_shot(kernel):
+    """A prompt prefilled in three chunks through the cache gives the rows of
+    the one-shot causal prefill (bottom-right alignment)."""
+    L, P, h, hk, d = 900, 16, 8, 2, 128
+    q, cache, cu = _case([L], [L], h, hk, d, P, torch.float16, seed=9)
+    full = paged_prefill_attention(q, cache, cu, L, causal=True)
+    parts = []
+    for lo, hi in ((0, 300), (300, 301), (301, L)):
+        chunk = PagedKVCache(cache.k_cache, cache.v_cache, cache.page_table,
+                             torch.tensor([hi], dtype=torch.int32, device=DEV), P)
+        ccu = torch.tensor([0, hi - lo], dtype=torch.int32, device=DEV)
+        parts.append(paged_prefill_attention(q[lo:hi].contiguous(), chunk, ccu, hi - lo, causal=True))
+    torch.cuda.synchronize()
+    got = torch.cat(parts)
+    # both sides are kernel outputs, each within 2e-3 of the oracle
+    assert_parity(got, full.float(), tol=4e-3, label="chunked vs one-shot")
+    assert_parity(got, _ref32(q, cache, cu, True), label="chunked vs oracle")
+
+
+def test_paged_prefill_validation():
+    lens_k, lens_q = [10, 20], [4, 25]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 64, 16, torch.float16, seed=1)
+    with pytest.raises(ValueError, match="kv_len >= q_len"):
+        paged_prefill_attention(q, cache, cu, 25, causal=True)
+    out = paged_prefill_attention(q, cache, cu, 25, causal=False)  # allowed without causal masking
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache, cu, False), label="non-causal q_len > kv_len")
+    with pytest.raises(ValueError, match="max_seqlen_q"):
+        paged_prefill_attention(q, cache, cu, 5, causal=False)
+    bad = PagedKVCache(cache.k_cache, cache.v_cache, cache.page_table.clone(), cache.seq_lens, 16)
+    bad.page_table[1, 0] = cache.num_pages
+    with pytest.raises(AssertionError, match="references page"):
+        paged_prefill_attention(q, bad, cu, 25, causal=False)
+    with pytest.raises(ValueError, match="batch \\+ 1"):
+        paged_prefill_attention(q, cache, cu[:2], 25, causal=False)
+
+
+@pytest.mark.parametrize("P", [32, 64])
+def test_paged_prefill_row_modes_agree(P, monkeypatch):
+    """Pages of >= 16 rows take the wave-uniform addressing; forcing the
+    per-lane addressing on the same inputs must give identical bits."""
+    lens_k, lens_q = [900, 70, 129], [300, 70, 1]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, P, torch.bfloat16, seed=P + 1)
+    uni = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    monkeypatch.setenv("FAT_PREFILL_PAGED_ROWS", "lane")
+    lane = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(uni, lane)
+    assert_parity(uni, _ref32(q, cache, cu, True), label=f"paged P{P} uniform rows")
+
+
+def test_paged_prefill_ignores_nan_past_seq_len(kernel):
+    """Slots past each sequence's end hold NaN: the kernel must never let them
+    into the result (the wave-uniform path zeroes those rows before LDS)."""
+    lens_k, lens_q = [100, 37, 64], [100, 5, 64]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, 32, torch.float16, seed=3)
+    for b, n in enumerate(lens_k):
+        pages = (n + 31) // 32
+        last = int(cache.page_table[b, pages - 1])
+        used = n - (pages - 1) * 32
+        if used < 32:
+            cache.k_cache[last, used:] = float("nan")
+            cache.v_cache[last, used:] = float("nan")
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    assert_parity(out, _ref32(q, cache, cu, True), label="NaN past seq_len")
+
+
+def test_prefill_paged_op_and_backend_route():
+    """The extension op and the backend's paged-prefill route run the same
+    kernel as the function (also under torch.compile(fullgraph=True))."""
+    from flashattntile_amd.backend import AttentionMetadata, FlashAttnTileBackend
+
+    lens_k, lens_q = [300, 77], [20, 77]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, 16, torch.float16, seed=77)
+    want = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, softmax_scale=0.09)
+
+    def op(x):
+        return torch.ops.flashattn_tile.prefill_paged(x, cache.k_cache, cache.v_cache, cache.page_table,
+                                                      cache.seq_lens, cu, max(lens_q), 16, True, 0.09)
+
+    got = op(q)
+    compiled = torch.compile(op, fullgraph=True)(q)
+    backend = FlashAttnTileBackend(num_heads=8, num_kv_heads=2, head_dim=128, page_size=16)
+    routed = backend.forward(q, cache, AttentionMetadata(is_prefill=True, paged_prefill=True, cu_seqlens_q=cu,
+                                                         max_seqlen_q=max(lens_q), softmax_scale=0.09))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(compiled, want) and torch.equal(routed, want)

@@ -60,6 +60,17 @@ def test_fake_prefill_varlen_shapes():
     assert out.shape == (11, 4, 8) and out.device.type == "meta"
 
 
+def test_fake_prefill_paged_shapes():
+    with torch._subclasses.fake_tensor.FakeTensorMode():
+        q = torch.empty(11, 4, 8, device="meta")
+        k = torch.empty(12, 16, 2, 8, device="meta")
+        pt = torch.empty(2, 3, dtype=torch.int32, device="meta")
+        sl = torch.full((2,), 9, dtype=torch.int32, device="meta")
+        cu = torch.full((3,), 0, dtype=torch.int32, device="meta")
+        out = torch.ops.flashattn_tile.prefill_paged(q, k, k, pt, sl, cu, 7, 16, True, 0.35)
+    assert out.shape == (11, 4, 8) and out.device.type == "meta"
+
+
 def test_compile_fullgraph_has_zero_graph_breaks():
     """Traced on meta tensors so no kernel runs on this CPU-only host; the GPU
     suite compiles and runs the same function on the device."""
@@ -76,7 +87,11 @@ def test_compile_fullgraph_has_zero_graph_breaks():
     def pre(x):
         return torch.ops.flashattn_tile.prefill_varlen(x, kv, kv, cu, cu, 6, 6, True, 0.35) + 1
 
-    for fn, arg in ((dec, q), (pre, torch.empty(9, 4, 8, device="meta", dtype=torch.float16))):
+    def pre_paged(x):
+        return torch.ops.flashattn_tile.prefill_paged(x, k, k, pt, sl, cu, 6, 16, True, 0.35) - 1
+
+    pre_arg = torch.empty(9, 4, 8, device="meta", dtype=torch.float16)
+    for fn, arg in ((dec, q), (pre, pre_arg), (pre_paged, pre_arg)):
         explanation = torch._dynamo.explain(fn)(arg)
         assert explanation.graph_break_count == 0, explanation.break_reasons
         assert explanation.graph_count == 1
@@ -98,6 +113,9 @@ def test_cpu_tensors_raise_instead_of_falling_back():
     cu = torch.tensor([0, 3, 9], dtype=torch.int32)
     with pytest.raises(RuntimeError, match="ROCm device"):
         fat.prefill_attention(qp, kp, kp, cu, cu, max(lens), max(lens))
+    cache2 = _cache(batch=2, length=6, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fat.paged_prefill_attention(qp, cache2, cu, 6)
 
 
 def test_backend_kv_cache_shape_matches_allocate():
@@ -125,6 +143,14 @@ def test_backend_validation_and_routing_errors():
     with pytest.raises(ValueError, match="attn_metadata.k"):
         backend.forward(torch.randn(3, 4, 8), cache, AttentionMetadata(is_prefill=True, cu_seqlens_q=cu,
                                                                        cu_seqlens_k=cu))
+    # Paged prefill routing (extension field) needs only cu_seqlens_q and
+    # reaches the kernel wrapper, which refuses CPU tensors.
+    with pytest.raises(ValueError, match="cu_seqlens_q"):
+        backend.forward(torch.randn(3, 4, 8), cache, AttentionMetadata(is_prefill=True, paged_prefill=True))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        backend.forward(torch.randn(2, 4, 8), cache, AttentionMetadata(is_prefill=True, paged_prefill=True,
+                                                                       cu_seqlens_q=torch.tensor(
+                                                                           [0, 1, 2], dtype=torch.int32)))
     # Decode routing reaches the kernel wrapper, which refuses CPU tensors.
     with pytest.raises(RuntimeError, match="ROCm device"):
         backend.forward(torch.randn(2, 1, 4, 8), cache, AttentionMetadata(softmax_scale=0.35))

@@ -286,3 +286,72 @@ def test_planted_merge_mistake_is_caught():
     parts = R.lse_partials(q, k, v, [(0, 7), (7, 20)], 1.0)
     whole = R.lse_merge(R.lse_partials(q, k, v, [(0, 20)], 1.0))
     assert not torch.allclose(bad_merge(parts), whole, atol=1e-4)
+
+
+def _pool_from_packed(k, v, lens, page_size, perm_seed=None):
+    """A paged pool holding packed per-sequence K/V, pages optionally permuted."""
+    import math as _m
+
+    pages = [_m.ceil(n / page_size) for n in lens]
+    num_pages = sum(pages)
+    kc = torch.zeros(num_pages, page_size, k.shape[1], k.shape[2], dtype=k.dtype)
+    vc = torch.zeros_like(kc)
+    order = torch.arange(num_pages)
+    if perm_seed is not None:
+        order = torch.randperm(num_pages, generator=torch.Generator().manual_seed(perm_seed))
+    table = torch.zeros(len(lens), max(pages), dtype=torch.int32)
+    at_page, at_tok = 0, 0
+    for b, n in enumerate(lens):
+        for i in range(pages[b]):
+            phys = int(order[at_page + i])
+            table[b, i] = phys
+            lo = at_tok + i * page_size
+            hi = min(at_tok + n, lo + page_size)
+            kc[phys, : hi - lo] = k[lo:hi]
+            vc[phys, : hi - lo] = v[lo:hi]
+        at_page += pages[b]
+        at_tok += n
+    return kc, vc, table, torch.tensor(lens, dtype=torch.int32)
+
+
+def test_paged_prefill_oracle_pins():
+    from oracle.reference import ref_attention_paged, ref_attention_paged_prefill, ref_attention_varlen
+
+    g = torch.Generator().manual_seed(31)
+    lens_k, lens_q = [5, 9, 1, 12], [2, 9, 1, 3]
+    h, hk, d, P = 4, 2, 8, 4
+    k = torch.randn(sum(lens_k), hk, d, generator=g)
+    v = torch.randn(sum(lens_k), hk, d, generator=g)
+    q = torch.randn(sum(lens_q), h, d, generator=g)
+    cu_q = [0]
+    for n in lens_q:
+        cu_q.append(cu_q[-1] + n)
+    cu_k = [0]
+    for n in lens_k:
+        cu_k.append(cu_k[-1] + n)
+    kc, vc, table, sl = _pool_from_packed(k, v, lens_k, P)
+    # 1. a pool holding the packed K/V in order: the varlen result itself
+    got = ref_attention_paged_prefill(q, kc, vc, table, sl, cu_q, causal=True)
+    assert torch.equal(got, ref_attention_varlen(q, k, v, cu_q, cu_k, causal=True))
+    # 2. page-table permutation invariance
+    kc2, vc2, table2, _ = _pool_from_packed(k, v, lens_k, P, perm_seed=4)
+    assert torch.equal(ref_attention_paged_prefill(q, kc2, vc2, table2, sl, cu_q, causal=True), got)
+    # 3. one query per sequence: the decode oracle
+    q1 = torch.randn(len(lens_k), h, d, generator=g)
+    cu1 = list(range(len(lens_k) + 1))
+    assert torch.equal(ref_attention_paged_prefill(q1, kc, vc, table, sl, cu1, causal=True),
+                       ref_attention_paged(q1, kc, vc, table, sl, causal=True))
+    # 4. chunking identity: a 12-token causal prompt as chunks [0, 7) and
+    # [7, 12) (kv lengths 7 and 12) gives the one-shot rows.  A top-left
+    # causal convention (shift 0) would fail this.
+    L = 12
+    qf = torch.randn(L, h, d, generator=g)
+    kf = torch.randn(L, hk, d, generator=g)
+    vf = torch.randn(L, hk, d, generator=g)
+    kcf, vcf, tf, _ = _pool_from_packed(kf, vf, [L], P)
+    one = ref_attention_paged_prefill(qf, kcf, vcf, tf, torch.tensor([L], dtype=torch.int32), [0, L])
+    c1 = ref_attention_paged_prefill(qf[:7], kcf, vcf, tf, torch.tensor([7], dtype=torch.int32), [0, 7])
+    c2 = ref_attention_paged_prefill(qf[7:], kcf, vcf, tf, torch.tensor([L], dtype=torch.int32), [0, 5])
+    torch.testing.assert_close(torch.cat([c1, c2]), one, rtol=0, atol=1e-6)
+    wrong = ref_attention_varlen(qf[7:], kf[:5], vf[:5], [0, 5], [0, 5], causal=True)  # shift dropped
+    assert (wrong - one[7:]).abs().max() > 1e-2
