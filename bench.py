@@ -449,6 +449,54 @@ def _paged_prefill_row(name, lens_k, lens_q, dtype, device, args, page=16, hq=32
                     "sample": f"{group} query heads / 1 KV head of sequence 0, min of {reps}"}}
 
 
+def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16):
+    """Multi-token decode (q_len = T) through fat_paged_decode: bytes = K/V
+    read once + T queries and outputs per sequence."""
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd import _hip
+    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
+    from oracle.reference import ref_attention_paged_prefill
+
+    q1, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, torch.float16, seed=13,
+                                                               device=device, copies=2)
+    gen = torch.Generator(device=device).manual_seed(14)
+    q = torch.randn(len(lens), T, hq, d, device=device, generator=gen).half()
+    out = torch.empty_like(q)
+    total_pages = sum(math.ceil(n / page) for n in lens)
+    sk, pps = decode_partition(len(lens), hq, hkv, table.shape[1], total_pages, q_len=T)
+    ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens) * T, hq, d, sk)), dtype=torch.uint8,
+                     device=device)
+    stream = torch.cuda.current_stream(device)
+    handle = int(stream.cuda_stream)
+
+    def step(i):
+        k, v, _, _ = pools[i % 2]
+        _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
+                          pages_per_split=pps)
+
+    ms = _time_steps(step, max(20, args.steps // 4), 5, stream)
+    nbytes = bytes_decode_paged(lens, hq, hkv, d) + 2 * len(lens) * (T - 1) * hq * d * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    k0, v0, _, _ = pools[0]
+    used = table_cpu[:1].flatten().unique().long()
+    kc, vc = k0[used.to(device)].cpu(), v0[used.to(device)].cpu()
+    remap = torch.full((k0.shape[0],), -1, dtype=torch.int64)
+    remap[used] = torch.arange(used.numel())
+    tab = remap[table_cpu[:1].long()].clamp_min(0).to(torch.int32)
+    qc = q[:1].reshape(T, hq, d).cpu()
+    best, reps = _time_cpu(lambda: ref_attention_paged_prefill(qc, kc, vc, tab, seq_cpu[:1], [0, T]),
+                           args.cpu_budget / 4)
+    cpu_bytes = bytes_decode_paged(lens[:1], hq, hkv, d) + 2 * (T - 1) * hq * d * 2
+    del pools
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "decode_multi", "value": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "pages_per_split": pps, "q_len": T,
+            "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
+                    "sample": f"1 of {len(lens)} sequences, min of {reps}"}}
+
+
 def _quantize_row(name, src_dtype, mode, device, args, pages=8192, page=16, hkv=8, d=128):
     """fat_quantize_pages over a whole K pool (the headline cache's 8192 pages);
     two pools alternate.  Bytes = read src + write codes + write scales."""
@@ -576,6 +624,9 @@ def all_configs(args, device):
     emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
     for page in (32, 64):
         emit(_decode_row(f"decode fp16 P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device, args, flush))
+    # Multi-token (speculative) decode: T query tokens per sequence
+    for T in (2, 4, 8):
+        emit(_multi_decode_row(f"decode fp16 multi-token T{T} B32 ctx4096", [4096] * 32, T, device, args))
     # Paged (chunked) prefill: K/V through the page table (page 16)
     for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         emit(_paged_prefill_row(f"prefill paged {dn} causal L8192 P16", [8192], [8192], dt, device, args))

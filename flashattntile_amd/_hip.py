@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enum fat_dtype
 DT_F16 = 0
@@ -85,6 +85,9 @@ class DecodeArgs(ctypes.Structure):
         ("kv_dtype", _c_i32),
         ("pages_per_split", _c_i32),
         ("softmax_scale", ctypes.c_float),
+        ("q_stride_t", _c_i64),
+        ("out_stride_t", _c_i64),
+        ("q_len", _c_i32),
     ]
 
 
@@ -346,7 +349,11 @@ def paged_decode(
     waves_per_group: int = 0,
     pages_per_split: int = 0,
 ) -> None:
-    """Enqueue ``fat_paged_decode`` for already-validated device tensors."""
+    """Enqueue ``fat_paged_decode`` for already-validated device tensors.
+
+    ``q``/``out`` are ``[B, H, D]`` (one query per sequence) or
+    ``[B, T, H, D]`` (multi-token decode, ``q_len = T``)."""
+    multi = q.dim() == 4
     a = DecodeArgs()
     a.q = _ptr(q)
     a.k_cache = _ptr(k_cache)
@@ -357,17 +364,22 @@ def paged_decode(
     a.seq_lens = _ptr(seq_lens)
     a.out = _ptr(out)
     a.workspace = _ptr(workspace)
-    a.q_stride_b, a.q_stride_h = q.stride(0), q.stride(1)
+    if multi:
+        a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+        a.out_stride_t = out.stride(1)
+        a.q_len = q.shape[1]
+    else:
+        a.q_stride_b, a.q_stride_h = q.stride(0), q.stride(1)
     a.k_stride_page, a.k_stride_slot, a.k_stride_head = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
     a.v_stride_page, a.v_stride_slot, a.v_stride_head = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
     if k_scale is not None:
         a.scale_stride_page, a.scale_stride_head = k_scale.stride(0), k_scale.stride(1)
     a.page_table_stride = page_table.stride(0)
-    a.out_stride_b, a.out_stride_h = out.stride(0), out.stride(1)
+    a.out_stride_b, a.out_stride_h = out.stride(0), out.stride(2 if multi else 1)
     a.batch = q.shape[0]
-    a.num_heads = q.shape[1]
+    a.num_heads = q.shape[-2]
     a.num_kv_heads = k_cache.shape[2]
-    a.head_dim = q.shape[2]
+    a.head_dim = q.shape[-1]
     a.page_size = int(page_size)
     a.num_pages = k_cache.shape[0]
     a.max_pages = page_table.shape[1]

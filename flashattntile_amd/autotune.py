@@ -137,7 +137,7 @@ def decode_heads_per_workgroup(group: int, quantized: bool = False) -> int:
 
 def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: int, total_pages: int,
                      num_cus: int = MI355X_CUS, min_pages_per_split: int = 8,
-                     max_split: int = 16, quantized: bool = False) -> tuple[int, int]:
+                     max_split: int = 16, quantized: bool = False, q_len: int = 1) -> tuple[int, int]:
     """``(split_k, pages_per_split)`` for a possibly ragged batch on MI355X.
 
     Every partition holds the same number of pages and split_k covers the
@@ -151,8 +151,9 @@ def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: i
     lengths in [16, 65536]).
     """
     group = max(1, num_heads // max(1, num_kv_heads))
-    heads_per_wg = decode_heads_per_workgroup(group, quantized)
-    groups = num_kv_heads * math.ceil(group / heads_per_wg)
+    rows = group * max(1, int(q_len))  # (query head, token) rows per KV head
+    heads_per_wg = 32 if q_len > 1 else decode_heads_per_workgroup(group, quantized)
+    groups = num_kv_heads * math.ceil(rows / heads_per_wg)
     max_pages = max(1, int(max_pages))
     total_pages = max(1, int(total_pages))
     skewed = batch * max_pages >= 2 * total_pages

@@ -21,7 +21,12 @@
 //     round_to_q_dtype(float(x) * scale), the reference's own
 //     dequantise-then-attend semantics (flashattn_tile/quant.py:145-161);
 //   * with split_k > 1 each workgroup writes (acc, m, l) for its partition
-//     and a second kernel merges the partitions by log-sum-exp.
+//     and a second kernel merges the partitions by log-sum-exp;
+//   * multi-token decode (q_len = T > 1, e.g. speculative verification) runs
+//     on the MFMA kernel: its 32 MFMA columns are (query head, token) rows,
+//     G * T of them per KV head, so each K/V page is still read once per KV
+//     head per 32 rows; token t sees keys j <= seq_len - T + t (the
+//     bottom-right causal convention of flashattn_tile/reference.py:19-22).
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -57,13 +62,14 @@ struct DecodeParams {
   uint8_t* out;
   float* ws_acc;  // [B, H, S, D]
   float* ws_ml;   // [B, H, S, 2]  (m in log2 units, l)
-  int64_t q_sb, q_sh;
+  int64_t q_sb, q_sh, q_st;
   int64_t k_sp, k_ss, k_sh;
   int64_t v_sp, v_ss, v_sh;
   int64_t sc_sp, sc_sh;
   int64_t pt_sb;
-  int64_t o_sb, o_sh;
+  int64_t o_sb, o_sh, o_st;
   int32_t H, Hkv, group, hg_per_kv;
+  int32_t T;  // query tokens per sequence (1 = single-query decode)
   int32_t P, log2P, num_pages, max_pages;
   int32_t pps_fixed;  // pages per partition, 0 = ceil(np / split_k)
   float scale_log2;  // softmax_scale * log2(e)
@@ -424,23 +430,28 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 // end, and partitions go through the same log-sum-exp merge as the VALU
 // kernel.  P is rounded to the K/V type for PV (bf16: hi + lo parts).
 // ---------------------------------------------------------------------------
-constexpr int kDecMfmaWaves = 4;
-
-template <typename QT, int KV, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NW = 4 or 8 waves per workgroup: the host takes 8 when the grid has fewer
+// than two workgroups per CU, so each CU still streams 8 blocks at a time.
+template <typename QT, int KV, int D, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void paged_decode_mfma_kernel(const DecodeParams p) {
-  constexpr int NW = kDecMfmaWaves;
-  constexpr int KS = D / 16;     // MFMA k-steps (= 16-byte K loads per lane)
+  constexpr int KS = D / 16;     // MFMA k-steps
   constexpr int DB = D / 32;     // 32-dim blocks of O^T
-  constexpr int HALF = D / 2;    // head dims owned by each lane half
-  constexpr int V_RS = D + 32;   // LDS row stride of the V tile (elements)
+  constexpr int K_RS = D + 8;    // LDS row strides (elements) of the K and V
+  constexpr int V_RS = D + 32;   // tiles, spreading reads over the banks
   constexpr bool SPLIT_P = std::is_same<QT, BF16>::value;
-  static_assert(KS * 8 == HALF, "lane loads must cover the half row");
   constexpr int EB = KV == KV_SAME ? 2 : 1;        // bytes per stored element
-  constexpr int NLD = HALF * EB / 16;              // 16-byte loads per lane per row half
+  // Row-coalesced loads: CPR lanes cover one stored row with 16-byte chunks
+  // (EPC elements each); one load instruction covers RPL rows, so a 32-key
+  // block takes NLD loads per lane for K and as many for V.
+  constexpr int EPC = 16 / EB;
+  constexpr int CPR = D / EPC;
+  constexpr int RPL = 64 / CPR;
+  constexpr int NLD = 32 / RPL;
+  static_assert(CPR * EPC == D && NLD * RPL == 32, "unsupported head_dim / element size");
 
-  // V tiles during the loop; per-wave O / m / l for the final merge after it.
-  constexpr int kTileBytes = NW * 32 * V_RS * 2;
+  // K and V tiles during the loop; per-wave O / m / l for the merge after it.
+  constexpr int kTileBytes = NW * 32 * (K_RS + V_RS) * 2;
   constexpr int kMergeBytes = (NW * 32 * D + NW * 32 * 2) * 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes];
 
@@ -450,13 +461,16 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
   const int b = blockIdx.z;
   const int sub = y % p.hg_per_kv;
   const int kvh = y / p.hg_per_kv;
-  const int head0 = kvh * p.group + sub * 32;
-  const int nvalid = min(32, p.group - sub * 32);
+  // The workgroup's 32 columns are rows r = sub * 32 + c of this KV head's
+  // group * T (query head, token) pairs: head kvh * group + r % group, token
+  // r / group (T = 1: the heads of the group).
+  const int row_base = sub * 32;
+  const int nvalid = min(32, p.group * p.T - row_base);
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int li = lane & 31;  // key row (A operand) / head column (B, S^T)
-  const int g = lane >> 5;   // k-group: head dims [g * HALF, g * HALF + HALF)
+  const int li = lane & 31;  // key row (A operand) / (head, token) column (B, S^T)
+  const int g = lane >> 5;   // k-group: head dims 16ks + 8g .. +7 of k-step ks
 
   int seq_len = p.lens[b];
   seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
@@ -467,72 +481,82 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
   const int t_begin = pb << p.log2P;
   const int t_end = min(seq_len, pe << p.log2P);
   const int n_blocks = t_end > t_begin ? (t_end - t_begin + 31) >> 5 : 0;
+  // This lane's column: (query head, token) and the end of its visible keys.
+  const int my_r = row_base + min(li, nvalid - 1);
+  const int my_t = my_r / p.group;
+  const int my_h = kvh * p.group + (my_r - my_t * p.group);
+  const int my_end = min(t_end, seq_len - p.T + 1 + my_t);
 
-  // Q^T: lane (head li, k-group g), k-step ks = head dims g*HALF + 8ks + 0..7.
+  // Q^T: lane (column li, k-group g), k-step ks = head dims 16ks + 8g + 0..7.
   u32x4 qf[KS];
   {
-    const int qh = head0 + min(li, nvalid - 1);
-    const uint8_t* qp = p.q + 2 * ((int64_t)b * p.q_sb + (int64_t)qh * p.q_sh + g * HALF);
+    const uint8_t* qp = p.q + 2 * ((int64_t)b * p.q_sb + (int64_t)my_t * p.q_st + (int64_t)my_h * p.q_sh + 8 * g);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
   }
 
   const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
-  // Raw K/V bytes of key (block base + li), head dims g*HALF.. (NLD
-  // contiguous 16-byte loads each) and, for 8-bit caches, that key's page
-  // scales.
+  const int lrow = lane / CPR;  // this lane's row inside each load
+  const int lcol = lane % CPR;  // and its 16-byte chunk
+  const int64_t koff = (int64_t)kvh * p.k_sh + lcol * EPC;
+  const int64_t voff = (int64_t)kvh * p.v_sh + lcol * EPC;
+  // Raw K/V chunks of a 32-key block: load i covers rows RPL*i .. RPL*i +
+  // RPL - 1, which lie in one page (page_size >= RPL), so its page id and
+  // (8-bit caches) scales are wave-uniform.  Rows past t_end re-read the last
+  // valid key; their scores are masked.
   struct Raw {
     u32x4 k[NLD], v[NLD];
-    float ksc, vsc;
+    float ksc[NLD], vsc[NLD];
   };
   auto fetch = [&](Raw& R, int blk) {
-    const int key = min(t_begin + (blk << 5) + li, t_end - 1);
-    int phys = ptrow[key >> p.log2P];
-    phys = min(max(phys, 0), p.num_pages - 1);
-    const int slot = key & (p.P - 1);
-    const uint8_t* kp = p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + (int64_t)kvh * p.k_sh + g * HALF);
-    const uint8_t* vp = p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + (int64_t)kvh * p.v_sh + g * HALF);
+    const int kb = t_begin + (blk << 5);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) {
-      R.k[j] = *reinterpret_cast<const u32x4*>(kp + 16 * j);
-      R.v[j] = *reinterpret_cast<const u32x4*>(vp + 16 * j);
-    }
-    if constexpr (KV != KV_SAME) {
-      R.ksc = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
-      R.vsc = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
-    } else {
-      R.ksc = R.vsc = 1.f;
+    for (int i = 0; i < NLD; ++i) {
+      int rs = kb + i * RPL;
+      if (rs >= t_end) rs = (t_end - 1) & ~(RPL - 1);
+      int phys = ptrow[rs >> p.log2P];
+      phys = min(max(phys, 0), p.num_pages - 1);
+      const int slot = min(rs + lrow, t_end - 1) & (p.P - 1);
+      R.k[i] = *reinterpret_cast<const u32x4*>(p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + koff));
+      R.v[i] = *reinterpret_cast<const u32x4*>(p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + voff));
+      if constexpr (KV != KV_SAME) {
+        R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+        R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
+      }
     }
   };
-  // MFMA operand words (QT pairs) of k-step ks from the raw bytes: copied for
+  // Store one raw chunk as QT elements at dst (EPC of them): a copy for
   // fp16/bf16 caches, round_to_QT(float(x) * scale) for 8-bit ones.
-  auto operand = [&](const u32x4* raw, float sc, int ks) -> u32x4 {
+  auto put = [&](uint16_t* dst, const u32x4& raw, float sc) {
     if constexpr (KV == KV_SAME) {
-      return raw[ks];
+      *reinterpret_cast<u32x4*>(dst) = raw;
     } else {
-      const u32 w0 = raw[ks >> 1][2 * (ks & 1)];
-      const u32 w1 = raw[ks >> 1][2 * (ks & 1) + 1];
-      float f[8];
-      if constexpr (KV == KV_I8) {
-        const float nb = -128.0f * sc;
-        i8x4_biased(w0, f);
-        i8x4_biased(w1, f + 4);
+      const float nb = -128.0f * sc;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], sc, nb);
-      } else {
-        fp8x4(w0, f);
-        fp8x4(w1, f + 4);
+      for (int h2 = 0; h2 < 2; ++h2) {
+        u32x4 o;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = f[e] * sc;
+        for (int j = 0; j < 2; ++j) {
+          float f[4];
+          if constexpr (KV == KV_I8) {
+            i8x4_biased(raw[2 * h2 + j], f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = __builtin_fmaf(f[e], sc, nb);
+          } else {
+            fp8x4(raw[2 * h2 + j], f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = f[e] * sc;
+          }
+          o[2 * j] = Pair<QT>::pack(f[0], f[1]);
+          o[2 * j + 1] = Pair<QT>::pack(f[2], f[3]);
+        }
+        *reinterpret_cast<u32x4*>(dst + 8 * h2) = o;
       }
-      u32x4 o;
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) o[e2] = Pair<QT>::pack(f[2 * e2], f[2 * e2 + 1]);
-      return o;
     }
   };
 
-  uint16_t* const Vt = reinterpret_cast<uint16_t*>(smem) + w * 32 * V_RS;
+  uint16_t* const Kt = reinterpret_cast<uint16_t*>(smem) + w * 32 * (K_RS + V_RS);
+  uint16_t* const Vt = Kt + 32 * K_RS;
   const int tr_c = (lane & 15) >> 2;
   const int tr_j = lane & 3;
   const int tr_G = lane >> 4;
@@ -550,28 +574,33 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 
   // One 32-key block from R; refills R with block nxt once R is consumed.
   auto compute = [&](Raw& R, int blk, int nxt) {
-    // V(blk) into this wave's LDS tile (row = key, columns = head dims).
+    // K(blk) and V(blk) into this wave's LDS tiles (row = key, columns =
+    // head dims), then R is free for the next block's loads.
 #pragma unroll
-    for (int j = 0; j < KS; ++j)
-      *reinterpret_cast<u32x4*>(&Vt[li * V_RS + g * HALF + 8 * j]) = operand(R.v, R.vsc, j);
-    // S^T = K Q^T for the 32 keys of this block.
-    u32x4 kop[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kop[ks] = operand(R.k, R.ksc, ks);
-    if (nxt < n_blocks) fetch(R, nxt);  // R is free once its K/V operands are built
+    for (int i = 0; i < NLD; ++i) {
+      const int row = i * RPL + lrow;
+      put(&Kt[row * K_RS + lcol * EPC], R.k[i], R.ksc[i]);
+      put(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
+    }
+    if (nxt < n_blocks) fetch(R, nxt);
+    wave_lds_fence();
+    // S^T = K Q^T for the 32 keys of this block: A = K rows li, dims 16ks + 8g.
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = Mfma<QT>::mma(kop[ks], qf[ks], s);
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(&Kt[li * K_RS + 16 * ks + 8 * g]);
+      s = Mfma<QT>::mma(a, qf[ks], s);
+    }
 
-    // Online softmax for head li over keys kb + (r&3) + 4g + 8(r>>2).
+    // Online softmax for column li over keys kb + (r&3) + 4g + 8(r>>2).
     const int kb = t_begin + (blk << 5);
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb + (r & 3) + 4 * g + 8 * (r >> 2);
-      const float x = key < t_end ? s[r] * c : -INFINITY;
+      const float x = key < my_end ? s[r] * c : -INFINITY;
       s[r] = x;
       mx = fmaxf(mx, x);
     }
@@ -586,13 +615,16 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
     }
+    // A column that has seen no visible key yet (only possible for T > 1)
+    // keeps m = -inf; its scores are -inf too, and exp2(-inf - 0) = 0.
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     u32x4 pf[2], pl[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const float x0 = fast_exp2(s[8 * t + 2 * e2] - m_run);
-        const float x1 = fast_exp2(s[8 * t + 2 * e2 + 1] - m_run);
+        const float x0 = fast_exp2(s[8 * t + 2 * e2] - m_use);
+        const float x1 = fast_exp2(s[8 * t + 2 * e2 + 1] - m_use);
         l_run += x0 + x1;
         const u32 hp = Pair<QT>::pack(x0, x1);
         pf[t][e2] = hp;
@@ -648,12 +680,14 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
         L = __builtin_fmaf(sml[(ww * 32 + hh) * 2 + 1], f, L);
       }
     }
-    const int h = head0 + hh;
+    const int rr = row_base + hh;
+    const int tt = rr / p.group;
+    const int h = kvh * p.group + (rr - tt * p.group);
     if (S == 1) {
-      uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + (b * p.o_sb + h * p.o_sh + d);
+      uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + (b * p.o_sb + tt * p.o_st + h * p.o_sh + d);
       *op = Pair<QT>::from_float(L > 0.f ? A / L : 0.f);
     } else {
-      const int64_t row = ((int64_t)b * p.H + h) * S + split;
+      const int64_t row = (((int64_t)b * p.T + tt) * p.H + h) * S + split;
       p.ws_acc[row * D + d] = A;
       if (d == 0) {
         p.ws_ml[row * 2 + 0] = M;
@@ -665,17 +699,20 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 
 // Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
 //   M = max_s m_s, w_s = 2^(m_s - M), o = sum_s acc_s w_s / sum_s l_s w_s.
+// Rows are (sequence, token, head) with T tokens per sequence.
 template <typename QT>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ ws_acc,
                                                            const float* __restrict__ ws_ml, uint8_t* out,
-                                                           int B, int H, int D, int S, int64_t o_sb,
-                                                           int64_t o_sh) {
+                                                           int B, int T, int H, int D, int S, int64_t o_sb,
+                                                           int64_t o_st, int64_t o_sh) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)B * H * D) return;
+  if (idx >= (int64_t)B * T * H * D) return;
   const int d = idx % D;
   const int64_t bh = idx / D;
   const int h = bh % H;
-  const int b = bh / H;
+  const int64_t bt = bh / H;
+  const int t = bt % T;
+  const int b = bt / T;
   const float* ml = ws_ml + bh * S * 2;
   const float* acc = ws_acc + bh * S * D + d;
   float M = -INFINITY;
@@ -689,7 +726,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     }
   }
   const float o = L > 0.f ? A / L : 0.f;
-  uint16_t* op = reinterpret_cast<uint16_t*>(out) + (b * o_sb + h * o_sh + d);
+  uint16_t* op = reinterpret_cast<uint16_t*>(out) + (b * o_sb + t * o_st + h * o_sh + d);
   *op = Pair<QT>::from_float(o);
 }
 
@@ -738,30 +775,40 @@ int launch_decode_q(const fat::DecodeParams& prm, int kv, int D, int HG, int nw,
 }
 
 
+template <typename QT, int KV, int NW>
+void launch_decode_mfma_kvw(const fat::DecodeParams& prm, int D, dim3 grid, hipStream_t stream) {
+  if (D == 128)
+    hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 128, NW>), grid, dim3(NW * 64), 0, stream, prm);
+  else
+    hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 64, NW>), grid, dim3(NW * 64), 0, stream, prm);
+}
+
 template <typename QT, int KV>
-void launch_decode_mfma_kv(const fat::DecodeParams& prm, int D, dim3 grid, hipStream_t stream) {
-  if (D == 128) hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 128>), grid, dim3(256), 0, stream, prm);
-  else hipLaunchKernelGGL((fat::paged_decode_mfma_kernel<QT, KV, 64>), grid, dim3(256), 0, stream, prm);
+void launch_decode_mfma_kv(const fat::DecodeParams& prm, int D, int nw, dim3 grid, hipStream_t stream) {
+  if (nw == 8) launch_decode_mfma_kvw<QT, KV, 8>(prm, D, grid, stream);
+  else launch_decode_mfma_kvw<QT, KV, 4>(prm, D, grid, stream);
 }
 
 template <typename QT>
-void launch_decode_mfma_q(const fat::DecodeParams& prm, int kv, int D, dim3 grid, hipStream_t stream) {
+void launch_decode_mfma_q(const fat::DecodeParams& prm, int kv, int D, int nw, dim3 grid, hipStream_t stream) {
   switch (kv) {
-    case fat::KV_SAME: launch_decode_mfma_kv<QT, fat::KV_SAME>(prm, D, grid, stream); break;
-    case fat::KV_I8: launch_decode_mfma_kv<QT, fat::KV_I8>(prm, D, grid, stream); break;
-    default: launch_decode_mfma_kv<QT, fat::KV_FP8>(prm, D, grid, stream); break;
+    case fat::KV_SAME: launch_decode_mfma_kv<QT, fat::KV_SAME>(prm, D, nw, grid, stream); break;
+    case fat::KV_I8: launch_decode_mfma_kv<QT, fat::KV_I8>(prm, D, nw, grid, stream); break;
+    default: launch_decode_mfma_kv<QT, fat::KV_FP8>(prm, D, nw, grid, stream); break;
   }
 }
 
 int launch_merge(const fat::DecodeParams& prm, const fat_decode_args* a, int D, hipStream_t stream) {
-  const int64_t n = (int64_t)a->batch * a->num_heads * D;
+  const int64_t n = (int64_t)a->batch * prm.T * a->num_heads * D;
   const dim3 mgrid((unsigned)((n + 255) / 256));
   if (a->q_dtype == FAT_DTYPE_F16) {
     hipLaunchKernelGGL(fat::decode_merge_kernel<fat::F16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+                       prm.out, a->batch, prm.T, a->num_heads, D, a->split_k, a->out_stride_b, prm.o_st,
+                       a->out_stride_h);
   } else {
     hipLaunchKernelGGL(fat::decode_merge_kernel<fat::BF16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, a->num_heads, D, a->split_k, a->out_stride_b, a->out_stride_h);
+                       prm.out, a->batch, prm.T, a->num_heads, D, a->split_k, a->out_stride_b, prm.o_st,
+                       a->out_stride_h);
   }
   return fat_host::launch_status("decode_merge_kernel");
 }
@@ -837,10 +884,17 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     fat_host::set_error("fat_paged_decode: split_k > 1 needs a workspace");
     return FAT_E_INVALID;
   }
+  if (a->q_len < 0 || a->q_len > 64) {
+    fat_host::set_error("fat_paged_decode: q_len must be in [0, 64] (0 and 1 = one query per sequence), got %d",
+                        a->q_len);
+    return FAT_E_INVALID;
+  }
+  const int T = a->q_len > 1 ? a->q_len : 1;
   // 16-byte alignment of every row start the kernel loads.
   const int eb = (kv == fat::KV_SAME) ? 2 : 1;
   const uintptr_t align_or = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
                              (uintptr_t)(2 * a->q_stride_b) | (uintptr_t)(2 * a->q_stride_h) |
+                             (uintptr_t)(T > 1 ? 2 * a->q_stride_t : 0) |
                              (uintptr_t)(eb * a->k_stride_page) | (uintptr_t)(eb * a->k_stride_slot) |
                              (uintptr_t)(eb * a->k_stride_head) | (uintptr_t)(eb * a->v_stride_page) |
                              (uintptr_t)(eb * a->v_stride_slot) | (uintptr_t)(eb * a->v_stride_head);
@@ -855,8 +909,9 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     if (!strcmp(force, "mfma")) use_mfma = true;
     else if (!strcmp(force, "valu")) use_mfma = false;
   }
+  if (T > 1) use_mfma = true;  // only the MFMA kernel has per-token rows
   const int HG = use_mfma ? 32 : (group >= 8 ? 8 : 4);
-  const int hg_per_kv = (group + HG - 1) / HG;
+  const int hg_per_kv = (group * T + HG - 1) / HG;
 
   fat::DecodeParams prm{};
   prm.q = static_cast<const uint8_t*>(a->q);
@@ -867,11 +922,12 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   prm.pt = a->page_table;
   prm.lens = a->seq_lens;
   prm.out = static_cast<uint8_t*>(a->out);
-  const size_t acc_elems = (size_t)a->batch * a->num_heads * a->split_k * D;
+  const size_t acc_elems = (size_t)a->batch * T * a->num_heads * a->split_k * D;
   prm.ws_acc = a->split_k > 1 ? static_cast<float*>(a->workspace) : nullptr;
   prm.ws_ml = a->split_k > 1 ? static_cast<float*>(a->workspace) + acc_elems : nullptr;
   prm.q_sb = a->q_stride_b;
   prm.q_sh = a->q_stride_h;
+  prm.q_st = T > 1 ? a->q_stride_t : 0;
   prm.k_sp = a->k_stride_page;
   prm.k_ss = a->k_stride_slot;
   prm.k_sh = a->k_stride_head;
@@ -883,6 +939,8 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   prm.pt_sb = a->page_table_stride;
   prm.o_sb = a->out_stride_b;
   prm.o_sh = a->out_stride_h;
+  prm.o_st = T > 1 ? a->out_stride_t : 0;
+  prm.T = T;
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = group;
@@ -896,16 +954,24 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const dim3 grid(a->split_k, a->num_kv_heads * hg_per_kv, a->batch);
+  const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
   if (use_mfma) {
-    if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, grid, stream);
-    else launch_decode_mfma_q<fat::BF16>(prm, kv, D, grid, stream);
+    // 8 waves per workgroup pay off only when the grid leaves CUs short of
+    // workgroups and each partition is long (>= 2048 keys, measured on
+    // MI355X); short partitions finish sooner with 4.
+    const int64_t pages_per_wg =
+        a->pages_per_split > 0 ? a->pages_per_split : ((int64_t)a->max_pages + a->split_k - 1) / a->split_k;
+    int nw = a->waves_per_group ? a->waves_per_group
+                                : ((wgs < 2 * 256 && pages_per_wg * a->page_size >= 2048) ? 8 : 4);
+    if (const char* force = getenv("FAT_DECODE_MFMA_WAVES")) nw = atoi(force) == 8 ? 8 : 4;
+    if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, nw, grid, stream);
+    else launch_decode_mfma_q<fat::BF16>(prm, kv, D, nw, grid, stream);
     const int rc = fat_host::launch_status("paged_decode_mfma_kernel");
     if (rc != FAT_OK || a->split_k == 1) return rc;
     return launch_merge(prm, a, D, stream);
   }
   // Fewer than two 4-wave workgroups per CU leave the MI355X's 256 CUs short
   // of loads in flight; use 8-wave workgroups then.
-  const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
   const int nw = a->waves_per_group ? a->waves_per_group : (wgs < 2 * 256 ? 8 : 4);
   int rc = (a->q_dtype == FAT_DTYPE_F16) ? launch_decode_q<fat::F16>(prm, kv, D, HG, nw, grid, stream)
                                          : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);

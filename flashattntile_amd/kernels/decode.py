@@ -5,7 +5,11 @@ Public functions keep the reference signatures and validation
 
 * :func:`paged_decode_attention` (fp16/bf16 cache, ``decode.py:533``);
 * :func:`paged_decode_attention_fp8` (int8 / float8_e4m3fn cache with
-  per-(page, KV-head) scales, ``decode.py:645``).
+  per-(page, KV-head) scales, ``decode.py:645``);
+
+plus :func:`paged_decode_attention_multi`, the multi-token (speculative)
+decode the reference lacks (its decode takes one query per sequence,
+``decode.py:548-553``).
 
 Differences, all deliberate:
 
@@ -34,6 +38,7 @@ __all__ = [
     "DEFAULT_CONFIG",
     "paged_decode_attention",
     "paged_decode_attention_fp8",
+    "paged_decode_attention_multi",
     "paged_decode_launch",
 ]
 
@@ -51,7 +56,7 @@ _QUANT_DTYPES = tuple(d for d in (torch.int8, getattr(torch, "float8_e4m3fn", No
 
 
 def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, max_len: int,
-                    total_pages: int) -> dict:
+                    total_pages: int, q_len: int = 1) -> dict:
     resolved = dict(DEFAULT_CONFIG)
     if config is not None:
         unknown = set(config) - set(DEFAULT_CONFIG)
@@ -60,8 +65,8 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, m
         resolved.update(config)
     if resolved["split_k"] is None:
         max_pages = -(-max_len // cache.page_size)
-        split, chunk = decode_partition(int(q.shape[0]), int(q.shape[1]), cache.num_kv_heads, max_pages,
-                                        total_pages, quantized=cache.k_cache.dtype in _QUANT_DTYPES)
+        split, chunk = decode_partition(int(q.shape[0]), int(q.shape[-2]), cache.num_kv_heads, max_pages,
+                                        total_pages, quantized=cache.k_cache.dtype in _QUANT_DTYPES, q_len=q_len)
         resolved["split_k"] = split
         if resolved["pages_per_split"] is None:
             resolved["pages_per_split"] = chunk
@@ -84,21 +89,26 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, m
     return resolved
 
 
-def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> tuple[int, int]:
+def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache, multi: bool = False) -> tuple[int, int]:
     """``decode.py:503-522`` + ``paging.validate_cache``, with one sync.
 
-    Returns ``(max_len, total_pages)`` for the partition heuristic."""
+    ``multi``: ``q`` is ``[batch, q_len, heads, head_dim]`` and every sequence
+    must already hold its q_len new tokens.  Returns ``(max_len,
+    total_pages)`` for the partition heuristic."""
     if not isinstance(cache, PagedKVCache):
         raise TypeError("cache must be a PagedKVCache")
     _check_layout(cache)
-    if q.dim() != 3:
+    if multi:
+        if q.dim() != 4:
+            raise ValueError(f"q must be [batch, q_len, heads, head_dim], got {tuple(q.shape)}")
+    elif q.dim() != 3:
         raise ValueError(f"q must be [batch, heads, head_dim], got {tuple(q.shape)}")
     if q.shape[0] != cache.batch_size:
         raise ValueError(f"q batch {q.shape[0]} != cache batch {cache.batch_size}")
-    if q.shape[2] != cache.head_dim:
-        raise ValueError(f"q head_dim {q.shape[2]} != cache head_dim {cache.head_dim}")
-    if q.shape[1] % cache.num_kv_heads != 0:
-        raise ValueError(f"num_heads {q.shape[1]} must be divisible by num_kv_heads {cache.num_kv_heads}")
+    if q.shape[-1] != cache.head_dim:
+        raise ValueError(f"q head_dim {q.shape[-1]} != cache head_dim {cache.head_dim}")
+    if q.shape[-2] % cache.num_kv_heads != 0:
+        raise ValueError(f"num_heads {q.shape[-2]} must be divisible by num_kv_heads {cache.num_kv_heads}")
     if q.device != cache.k_cache.device:
         raise ValueError("q and cache must live on the same device")
     if not q.is_floating_point():
@@ -116,6 +126,9 @@ def _validate_decode_inputs(q: torch.Tensor, cache: PagedKVCache) -> tuple[int, 
             raise AssertionError(f"page_table references page {hi} but cache has {cache.num_pages} pages")
     if min_len <= 0:
         raise ValueError("decode requires every sequence to hold at least one cached token")
+    if multi and min_len < q.shape[1]:
+        raise ValueError(f"multi-token decode requires every sequence to hold its {q.shape[1]} new tokens "
+                         f"(shortest seq_len {min_len})")
     return max_len, total_pages
 
 
@@ -141,7 +154,8 @@ def paged_decode_launch(
 ) -> torch.Tensor:
     """Enqueue the HIP decode without validation or synchronisation.
 
-    ``q`` must be contiguous fp16/bf16 on the cache's device; ``out`` (default
+    ``q`` (``[B, H, D]``, or ``[B, T, H, D]`` for multi-token decode) must be
+    contiguous fp16/bf16 on the cache's device; ``out`` (default
     ``empty_like(q)``) and ``workspace`` (default: allocated) may be passed in
     to avoid allocations.
     """
@@ -149,7 +163,8 @@ def paged_decode_launch(
         raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
     if out is None:
         out = torch.empty_like(q)
-    need = _hip.decode_workspace_bytes(q.shape[0], q.shape[1], q.shape[2], split_k)
+    rows = q.shape[0] * (q.shape[1] if q.dim() == 4 else 1)
+    need = _hip.decode_workspace_bytes(rows, q.shape[-2], q.shape[-1], split_k)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     k_scale = v_scale = None
@@ -227,3 +242,48 @@ def paged_decode_attention_fp8(
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"],
                                scales={"k": k_scale.contiguous(), "v": v_scale.contiguous()},
                                waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"])
+
+
+def paged_decode_attention_multi(
+    q: torch.Tensor,
+    cache: PagedKVCache,
+    softmax_scale: float | None = None,
+    config: dict | None = None,
+    scales=None,
+) -> torch.Tensor:
+    """Multi-token (speculative) decode: ``q`` ``[batch, q_len, num_heads,
+    head_dim]`` holds the last q_len tokens of each sequence, whose K/V are
+    already in ``cache`` (``seq_lens[b] >= q_len``).  Token t of sequence b
+    attends keys ``j <= seq_lens[b] - q_len + t`` -- the bottom-right causal
+    convention of :func:`~flashattntile_amd.kernels.prefill.prefill_attention`
+    -- and every K/V page is read once per KV head (per 32 (head, token)
+    rows) by the MFMA decode kernel.  ``scales`` (QuantScales or
+    ``{"k", "v"}``) selects an int8/float8_e4m3fn cache.  ``config`` as for
+    :func:`paged_decode_attention`.  Returns ``q``'s shape and dtype.
+    """
+    max_len, total_pages = _validate_decode_inputs(q, cache, multi=True)
+    q_len = int(q.shape[1])
+    if q_len > 64:
+        raise ValueError(f"multi-token decode takes at most 64 tokens per sequence, got {q_len}")
+    quantized = cache.k_cache.dtype in _QUANT_DTYPES
+    if quantized != (scales is not None):
+        raise ValueError("an int8/float8 cache needs scales, and only such a cache takes them")
+    scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+    cfg = _resolve_config(config, q, cache, max_len, total_pages, q_len=q_len)
+    _require_rocm(q, cache, "paged_decode_attention_multi")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"paged_decode_attention_multi: dtype {q.dtype} is not fp16/bf16")
+    sc = None
+    if quantized:
+        k_scale = scales["k"] if isinstance(scales, dict) else scales.k
+        v_scale = scales["v"] if isinstance(scales, dict) else scales.v
+        expected = (cache.num_pages, cache.num_kv_heads)
+        if tuple(k_scale.shape) != expected or tuple(v_scale.shape) != expected:
+            raise ValueError(f"scales must have shape {expected}, got {tuple(k_scale.shape)}")
+        if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
+            raise ValueError("scales must be float32")
+        sc = {"k": k_scale.contiguous(), "v": v_scale.contiguous()}
+    elif cache.k_cache.dtype != q.dtype:
+        raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
+    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], scales=sc,
+                               pages_per_split=cfg["pages_per_split"])

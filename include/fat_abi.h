@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 4
+#define FAT_ABI_VERSION 5
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -120,6 +120,15 @@ typedef struct fat_decode_args {
   int32_t kv_dtype; /* q_dtype, FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3           */
   int32_t pages_per_split; /* 0 = ceil(pages / split_k) per sequence        */
   float softmax_scale;
+  /* Multi-token decode (q_len > 1): q and out are [batch, q_len, num_heads,
+   * head_dim] with token strides q_stride_t / out_stride_t; token t of
+   * sequence b sees keys j <= seq_lens[b] - q_len + t (bottom-right causal,
+   * as fat_prefill_paged).  q_len 0 or 1 is single-query decode and the
+   * token strides are ignored.  The split-K workspace then holds
+   * batch * q_len rows: size it with fat_paged_decode_workspace_bytes(
+   * batch * q_len, ...).  At most 64 tokens. */
+  int64_t q_stride_t, out_stride_t;
+  int32_t q_len;
 } fat_decode_args;
 
 /*

@@ -27,11 +27,14 @@ ODD_LENS = [1, 17, 255, 1000]
 GQA = [(8, 8), (8, 2), (8, 1), (32, 8), (32, 1)]
 
 
-@pytest.fixture(params=["auto", "valu", "mfma"])
+@pytest.fixture(params=["auto", "valu", "mfma", "mfma8"])
 def decode_kernel(request, monkeypatch):
-    """Run with the library's choice and with each decode kernel forced (the
-    MFMA decode serves fp16/bf16 caches; 8-bit caches always take the VALU one)."""
-    monkeypatch.setenv("FAT_DECODE_KERNEL", request.param)
+    """Run with the library's choice and with each decode kernel forced: the
+    VALU decode, and the MFMA decode with 4 and with 8 waves per workgroup
+    (the library picks 8 only for long partitions in small grids)."""
+    monkeypatch.setenv("FAT_DECODE_KERNEL", request.param[:4])
+    if request.param == "mfma8":
+        monkeypatch.setenv("FAT_DECODE_MFMA_WAVES", "8")
     return request.param
 
 
