@@ -163,3 +163,23 @@ def test_append_argument_errors_are_reported():
     # Empty batch: nothing to launch, success.
     a.quant_dtype, a.batch = _hip.DT_FP8E4M3, 0
     assert lib.fat_append_kv(ctypes.byref(a), None) == 0 and _err() == ""
+
+
+def test_integration_stubs_match_the_abi():
+    """The ctypes stubs shown in INTEGRATION.md lay out their structs exactly
+    as the bindings (and so the header) do."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    found = 0
+    for block in re.findall(r"```python\n(.*?)```", text, re.S):
+        for cls in ("DecodeArgs", "AppendArgs"):
+            m = re.search(rf"class {cls}\(ctypes.Structure\):.*?\n\n", block, re.S)
+            if not m:
+                continue
+            ns = {"ctypes": ctypes}
+            exec(m.group(0), ns)  # the documentation's own struct definition
+            stub, mine = ns[cls], getattr(_hip, cls)
+            assert ctypes.sizeof(stub) == ctypes.sizeof(mine), cls
+            for name, _ in mine._fields_:
+                assert getattr(stub, name).offset == getattr(mine, name).offset, (cls, name)
+            found += 1
+    assert found == 2
