@@ -10,8 +10,9 @@ Infinity Cache cannot serve a step from the previous one.
 
 A step is one ``fat_paged_decode`` call through the C ABI (the decode
 kernel, plus the log-sum-exp merge kernel when split_k > 1); HIP events on
-the launch stream bracket the K timed steps.  split_k comes from the
-library's MI355X heuristic (``--tune`` times a few candidates instead).  The
+the launch stream bracket the K timed steps.  The launch (split_k, waves,
+kernel) is the one the decode wrappers make for this shape: the tuned store's
+entry, else the MI355X heuristic (``--tune`` times a few candidates).  The
 prefill leg (causal varlen, seq 8192, 32/8 heads, D128, fp16 and bf16) is
 reported under ``prefill`` with its own MFMA roofline.  ``cpu_baseline``
 times the fp32 oracle (oracle/reference.py) on a bounded sample of the
@@ -185,9 +186,37 @@ def _time_cpu(fn, budget_s, max_reps=21):
 # ---------------------------------------------------------------------------
 # Headline legs
 # ---------------------------------------------------------------------------
+def _product_launch(q, pools, table, lens, page, max_len, total_pages, q_len=1):
+    """What the decode wrappers launch for this shape (tuned store, else the
+    heuristic): (split_k, pages_per_split, waves or 0, kernel code, source)."""
+    from flashattntile_amd import PagedKVCache, _hip
+    from flashattntile_amd.autotune import best_config, decode_signature
+    from flashattntile_amd.kernels.decode import resolve_decode_config
+
+    k, v = pools[0][0], pools[0][1]
+    cache = PagedKVCache(k, v, table, lens, page)
+    cfg = resolve_decode_config(q, cache, max_len, total_pages, q_len=q_len)
+    sig = decode_signature(q.shape[0], q.shape[-2], k.shape[2], q.shape[-1], page, max_len, total_pages, k.dtype,
+                           q_len)
+    source = "tuned store" if best_config("decode", sig) else "heuristic"
+    code = {None: _hip.KERNEL_AUTO, "valu": _hip.KERNEL_DECODE_VALU, "mfma": _hip.KERNEL_DECODE_MFMA}[cfg["kernel"]]
+    return cfg["split_k"], cfg["pages_per_split"], cfg["num_warps"] or 0, code, source
+
+
+def _auto_waves(kernel, batch, group, hkv, split, pps, max_pages, page):
+    """Waves per workgroup the library picks when none is requested
+    (fat_paged_decode in csrc/decode.hip)."""
+    mfma = kernel == 2 or (kernel == 0 and group >= 8)
+    wgs = split * hkv * batch * (-(-group // 32) if mfma else 1)
+    per_wg = pps if pps > 0 else -(-max_pages // split)
+    if not mfma:
+        return 8 if wgs < 512 or per_wg * page >= 1024 else 4
+    return 8 if wgs < 512 and per_wg * page >= 2048 else 4
+
+
 def bench_decode(args, device):
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
+    from flashattntile_amd.autotune import bytes_decode_paged
 
     B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
     q, pools, table, lens, _, _ = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device=device,
@@ -200,28 +229,31 @@ def bench_decode(args, device):
     ws = torch.empty(_hip.decode_workspace_bytes(B, HQ, D, 64), dtype=torch.uint8, device=device)
 
     pages = (CTX + P - 1) // P
-    auto_split, auto_chunk = decode_partition(B, HQ, HKV, pages, B * pages)
+    auto_split, auto_chunk, auto_waves, auto_kernel, source = _product_launch(q, pools, table, lens, P, CTX,
+                                                                               B * pages)
 
-    def make(split, waves):
+    def make(split, waves, kernel):
         pps = auto_chunk if split == auto_split else 0
 
         def step(i):
             k, v, _, _ = pools[i % len(pools)]
             _hip.paged_decode(q, k, v, table, lens, out, P, scale, split, workspace=ws, stream=handle,
-                              waves_per_group=waves, pages_per_split=pps)
+                              waves_per_group=waves, pages_per_split=pps, kernel=kernel)
         return step
 
     if args.tune:
-        cands = [(s, w) for s in (1, 2, 3, 4, 8) for w in (4, 8)]
+        cands = [(s, w, auto_kernel) for s in (1, 2, 3, 4, 8) for w in (4, 8)]
+    elif args.split_k or args.waves:
+        cands = [(args.split_k or auto_split, args.waves or auto_waves, auto_kernel)]
     else:
-        cands = [(args.split_k or auto_split, args.waves or 0)]
+        cands = [(auto_split, auto_waves, auto_kernel)]
     tuning = {}
     if len(cands) > 1:
         for cand in cands:
             tuning[cand] = _time_steps(make(*cand), max(5, args.warmup // 4), 2, stream)
-    s, w = min(tuning, key=tuning.get) if tuning else cands[0]
+    s, w, kern = min(tuning, key=tuning.get) if tuning else cands[0]
     torch.cuda.synchronize()
-    ms = _time_steps(make(s, w), args.steps, args.warmup, stream)
+    ms = _time_steps(make(s, w, kern), args.steps, args.warmup, stream)
     gbs = nbytes / (ms * 1e-3) / 1e9
     del pools
     return {
@@ -229,8 +261,11 @@ def bench_decode(args, device):
         "gbs": gbs,
         "bytes": nbytes,
         "split_k": s,
-        "waves_per_group": w or (8 if B * HKV * s < 512 else 4),
-        "tuning_ms": {f"sk{a}_w{b}": round(t, 5) for (a, b), t in tuning.items()},
+        "waves_per_group": w or _auto_waves(kern, B, HQ // HKV, HKV, s, auto_chunk if s == auto_split else 0,
+                                            pages, P),
+        "kernel": {0: "auto", 1: "valu", 2: "mfma"}[kern],
+        "config_source": source if not (args.tune or args.split_k or args.waves) else "command line",
+        "tuning_ms": {f"sk{a}_w{b}": round(t, 5) for (a, b, _), t in tuning.items()},
         "shape": {"batch": B, "ctx": CTX, "num_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "page_size": P},
     }
 
@@ -314,7 +349,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
+    from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
     kv_elem = 1 if quant else 2
@@ -324,10 +359,11 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
                                                              device=device, copies=copies, quant=quant)
     maxp = table.shape[1]
     total_pages = sum(math.ceil(n / page) for n in lens)
+    waves, kern, source = 0, 0, "command line"
     if split:
         sk, pps = split, 0
     else:
-        sk, pps = decode_partition(len(lens), hq, hkv, maxp, total_pages, quantized=bool(quant))
+        sk, pps, waves, kern, source = _product_launch(q, pools, table, seq, page, max(lens), total_pages)
     out = torch.empty_like(q)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens), hq, d, sk)), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device)
@@ -336,7 +372,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     def step(i):
         k, v, ks, vs = pools[i % copies]
         _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
-                          k_scale=ks, v_scale=vs, pages_per_split=pps)
+                          k_scale=ks, v_scale=vs, pages_per_split=pps, waves_per_group=waves, kernel=kern)
 
     steps = max(20, args.steps // 4)
     if pool_bytes * copies < 2 * MALL_BYTES:
@@ -367,7 +403,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     torch.cuda.empty_cache()
     return {"config": name, "kind": "decode", "value": round(gbs, 1), "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
-            "pages_per_split": pps,
+            "pages_per_split": pps, "launch": {"waves": waves, "kernel": kern, "source": source},
             "timing": timing,
             "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
                     "sample": f"{nb} of {len(lens)} sequences, min of {reps}"}}
@@ -455,7 +491,7 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
-    from flashattntile_amd.autotune import bytes_decode_paged, decode_partition
+    from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged_prefill
 
     q1, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, torch.float16, seed=13,
@@ -464,7 +500,7 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     q = torch.randn(len(lens), T, hq, d, device=device, generator=gen).half()
     out = torch.empty_like(q)
     total_pages = sum(math.ceil(n / page) for n in lens)
-    sk, pps = decode_partition(len(lens), hq, hkv, table.shape[1], total_pages, q_len=T)
+    sk, pps, waves, kern, source = _product_launch(q, pools, table, seq, page, max(lens), total_pages, q_len=T)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens) * T, hq, d, sk)), dtype=torch.uint8,
                      device=device)
     stream = torch.cuda.current_stream(device)
@@ -473,7 +509,7 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     def step(i):
         k, v, _, _ = pools[i % 2]
         _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
-                          pages_per_split=pps)
+                          pages_per_split=pps, waves_per_group=waves, kernel=kern)
 
     ms = _time_steps(step, max(20, args.steps // 4), 5, stream)
     nbytes = bytes_decode_paged(lens, hq, hkv, d) + 2 * len(lens) * (T - 1) * hq * d * 2
@@ -492,7 +528,7 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     torch.cuda.empty_cache()
     return {"config": name, "kind": "decode_multi", "value": round(gbs, 1), "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
-            "pages_per_split": pps, "q_len": T,
+            "pages_per_split": pps, "q_len": T, "launch": {"waves": waves, "kernel": kern, "source": source},
             "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
                     "sample": f"1 of {len(lens)} sequences, min of {reps}"}}
 
@@ -616,6 +652,7 @@ def all_configs(args, device):
     # stress
     emit(_decode_row("decode fp16 B1 ctx131072 split16", [131072], 32, 8, 128, 16, device, args, flush, split=16,
                      cpu_seqs=1))
+    emit(_decode_row("decode fp16 B1 ctx131072", [131072], 32, 8, 128, 16, device, args, flush, cpu_seqs=1))
     g = torch.Generator().manual_seed(64)
     skew = [int(math.exp(x)) for x in (torch.rand(64, generator=g) * (math.log(65536) - math.log(16))
                                        + math.log(16)).tolist()]
@@ -725,6 +762,8 @@ def main():
             **dec["shape"],
             "split_k": dec["split_k"],
             "waves_per_group": dec["waves_per_group"],
+            "kernel": dec["kernel"],
+            "launch_from": dec["config_source"],
             "parallelism": "single GPU",
         },
         "roofline": {

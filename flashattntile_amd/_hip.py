@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # enum fat_dtype
 DT_F16 = 0
@@ -28,6 +28,13 @@ DT_BF16 = 1
 DT_I8 = 2
 DT_FP8E4M3 = 3
 DT_F32 = 4
+
+# enum fat_kernel (the `kernel` field of the decode and prefill arguments)
+KERNEL_AUTO = 0
+KERNEL_DECODE_VALU = 1
+KERNEL_DECODE_MFMA = 2
+KERNEL_PREFILL_PINGPONG = 1
+KERNEL_PREFILL_4WAVE = 2
 
 EXPORTED_SYMBOLS = (
     "fat_abi_version",
@@ -88,6 +95,7 @@ class DecodeArgs(ctypes.Structure):
         ("q_stride_t", _c_i64),
         ("out_stride_t", _c_i64),
         ("q_len", _c_i32),
+        ("kernel", _c_i32),
     ]
 
 
@@ -121,6 +129,7 @@ class PrefillArgs(ctypes.Structure):
         ("causal", _c_i32),
         ("dtype", _c_i32),
         ("softmax_scale", ctypes.c_float),
+        ("kernel", _c_i32),
     ]
 
 
@@ -158,6 +167,7 @@ class PrefillPagedArgs(ctypes.Structure):
         ("causal", _c_i32),
         ("dtype", _c_i32),
         ("softmax_scale", ctypes.c_float),
+        ("kernel", _c_i32),
     ]
 
 
@@ -348,6 +358,7 @@ def paged_decode(
     stream: int | None = None,
     waves_per_group: int = 0,
     pages_per_split: int = 0,
+    kernel: int = KERNEL_AUTO,
 ) -> None:
     """Enqueue ``fat_paged_decode`` for already-validated device tensors.
 
@@ -389,6 +400,7 @@ def paged_decode(
     a.kv_dtype = dtype_code(k_cache.dtype)
     a.pages_per_split = int(pages_per_split)
     a.softmax_scale = float(softmax_scale)
+    a.kernel = int(kernel)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
 
@@ -406,6 +418,7 @@ def prefill_varlen(
     softmax_scale: float,
     workspace: torch.Tensor | None = None,
     stream: int | None = None,
+    kernel: int = KERNEL_AUTO,
 ) -> None:
     """Enqueue ``fat_prefill_varlen`` for already-validated device tensors."""
     a = PrefillArgs()
@@ -431,6 +444,7 @@ def prefill_varlen(
     a.causal = 1 if causal else 0
     a.dtype = dtype_code(q.dtype)
     a.softmax_scale = float(softmax_scale)
+    a.kernel = int(kernel)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
 
@@ -448,6 +462,7 @@ def prefill_paged(
     causal: bool,
     softmax_scale: float,
     stream: int | None = None,
+    kernel: int = KERNEL_AUTO,
 ) -> None:
     """Enqueue ``fat_prefill_paged`` for already-validated device tensors."""
     a = PrefillPagedArgs()
@@ -475,6 +490,7 @@ def prefill_paged(
     a.causal = 1 if causal else 0
     a.dtype = dtype_code(q.dtype)
     a.softmax_scale = float(softmax_scale)
+    a.kernel = int(kernel)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_prefill_paged(ctypes.byref(a), _c_vp(handle)), "fat_prefill_paged")
 

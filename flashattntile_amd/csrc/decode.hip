@@ -890,6 +890,15 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     return FAT_E_INVALID;
   }
   const int T = a->q_len > 1 ? a->q_len : 1;
+  if (a->kernel != FAT_KERNEL_AUTO && a->kernel != FAT_KERNEL_DECODE_VALU && a->kernel != FAT_KERNEL_DECODE_MFMA) {
+    fat_host::set_error("fat_paged_decode: kernel must be FAT_KERNEL_AUTO (0), _DECODE_VALU (1) or _DECODE_MFMA (2), "
+                        "got %d", a->kernel);
+    return FAT_E_INVALID;
+  }
+  if (a->kernel == FAT_KERNEL_DECODE_VALU && T > 1) {
+    fat_host::set_error("fat_paged_decode: the VALU decode kernel takes one query per sequence (q_len %d)", T);
+    return FAT_E_UNSUPPORTED;
+  }
   // 16-byte alignment of every row start the kernel loads.
   const int eb = (kv == fat::KV_SAME) ? 2 : 1;
   const uintptr_t align_or = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
@@ -905,7 +914,9 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
 
   const int group = a->num_heads / a->num_kv_heads;
   bool use_mfma = group >= fat::kDecMfmaMinGroup || (kv != fat::KV_SAME && FAT_DEC_MFMA_8BIT);
-  if (const char* force = getenv("FAT_DECODE_KERNEL")) {
+  if (a->kernel != FAT_KERNEL_AUTO) {
+    use_mfma = a->kernel == FAT_KERNEL_DECODE_MFMA;
+  } else if (const char* force = getenv("FAT_DECODE_KERNEL")) {
     if (!strcmp(force, "mfma")) use_mfma = true;
     else if (!strcmp(force, "valu")) use_mfma = false;
   }
@@ -955,12 +966,12 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const dim3 grid(a->split_k, a->num_kv_heads * hg_per_kv, a->batch);
   const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
+  const int64_t pages_per_wg =
+      a->pages_per_split > 0 ? a->pages_per_split : ((int64_t)a->max_pages + a->split_k - 1) / a->split_k;
   if (use_mfma) {
     // 8 waves per workgroup pay off only when the grid leaves CUs short of
     // workgroups and each partition is long (>= 2048 keys, measured on
     // MI355X); short partitions finish sooner with 4.
-    const int64_t pages_per_wg =
-        a->pages_per_split > 0 ? a->pages_per_split : ((int64_t)a->max_pages + a->split_k - 1) / a->split_k;
     int nw = a->waves_per_group ? a->waves_per_group
                                 : ((wgs < 2 * 256 && pages_per_wg * a->page_size >= 2048) ? 8 : 4);
     if (const char* force = getenv("FAT_DECODE_MFMA_WAVES")) nw = atoi(force) == 8 ? 8 : 4;
@@ -970,9 +981,13 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     if (rc != FAT_OK || a->split_k == 1) return rc;
     return launch_merge(prm, a, D, stream);
   }
-  // Fewer than two 4-wave workgroups per CU leave the MI355X's 256 CUs short
-  // of loads in flight; use 8-wave workgroups then.
-  const int nw = a->waves_per_group ? a->waves_per_group : (wgs < 2 * 256 ? 8 : 4);
+  // 8-wave workgroups keep more loads in flight per CU.  They pay off when
+  // fewer than two 4-wave workgroups per CU leave the 256 CUs short of waves,
+  // and in any grid when each partition is long (>= 1024 keys: +8-12 % at
+  // B128, ctx 1024-16384, measured on MI355X); short partitions in big grids
+  // finish sooner with 4.
+  const int nw = a->waves_per_group ? a->waves_per_group
+                                    : ((wgs < 2 * 256 || pages_per_wg * a->page_size >= 1024) ? 8 : 4);
   int rc = (a->q_dtype == FAT_DTYPE_F16) ? launch_decode_q<fat::F16>(prm, kv, D, HG, nw, grid, stream)
                                          : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);
   if (rc != FAT_OK || a->split_k == 1) return rc;

@@ -899,17 +899,24 @@ int launch_prefill_t(const fat::PrefillParams& prm, bool causal, bool pingpong, 
   return fat_host::launch_status("prefill_kernel");
 }
 
+bool valid_prefill_kernel(int kernel) {
+  return kernel == FAT_KERNEL_AUTO || kernel == FAT_KERNEL_PREFILL_PINGPONG || kernel == FAT_KERNEL_PREFILL_4WAVE;
+}
+
 // Kernel choice and grid shared by fat_prefill_varlen and fat_prefill_paged.
 // The 8-wave ping-pong kernel needs a grid of at least FAT_PF_PP_MIN
 // 256-row workgroups to fill the chip; smaller problems use the 4-wave,
-// 128-row kernel (twice the workgroups).  FAT_PREFILL_KERNEL=pingpong|4wave
-// overrides the choice (tests exercise both kernels on every shape).
+// 128-row kernel (twice the workgroups).  A non-AUTO `kernel` argument forces
+// one of them; with AUTO, FAT_PREFILL_KERNEL=pingpong|4wave overrides the
+// choice (tests exercise both kernels on every shape).
 template <int PG>
 int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int dtype, int D, bool causal, float softmax_scale,
-                   const char* who, hipStream_t stream) {
+                   int kernel, const char* who, hipStream_t stream) {
   const int64_t nqb_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM;
   bool pingpong = nqb_pp * prm.B * prm.H >= FAT_PF_PP_MIN;
-  if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
+  if (kernel != FAT_KERNEL_AUTO) {
+    pingpong = kernel == FAT_KERNEL_PREFILL_PINGPONG;
+  } else if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
     if (!strcmp(force, "pingpong")) pingpong = true;
     else if (!strcmp(force, "4wave")) pingpong = false;
   }
@@ -962,6 +969,11 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
     fat_host::set_error("fat_prefill_varlen: dtype must be fp16 or bf16");
     return FAT_E_UNSUPPORTED;
   }
+  if (!valid_prefill_kernel(a->kernel)) {
+    fat_host::set_error("fat_prefill_varlen: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1) or "
+                        "_PREFILL_4WAVE (2), got %d", a->kernel);
+    return FAT_E_INVALID;
+  }
   const int D = a->head_dim;
   if (D != 64 && D != 128) {
     fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (64 or 128)", D);
@@ -1009,8 +1021,8 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = a->num_heads / a->num_kv_heads;
-  return launch_prefill<0>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
-                               "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
+  return launch_prefill<0>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
+                           "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
 }
 
 extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_ptr) {
@@ -1036,6 +1048,11 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16) {
     fat_host::set_error("fat_prefill_paged: dtype must be fp16 or bf16");
     return FAT_E_UNSUPPORTED;
+  }
+  if (!valid_prefill_kernel(a->kernel)) {
+    fat_host::set_error("fat_prefill_paged: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1) or "
+                        "_PREFILL_4WAVE (2), got %d", a->kernel);
+    return FAT_E_INVALID;
   }
   const int D = a->head_dim;
   if (D != 64 && D != 128) {
@@ -1103,8 +1120,8 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   if (uniform)
-    return launch_prefill<2>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
+    return launch_prefill<2>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
                              "fat_prefill_paged", stream);
-  return launch_prefill<1>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale,
+  return launch_prefill<1>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
                            "fat_prefill_paged", stream);
 }

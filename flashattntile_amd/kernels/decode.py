@@ -17,9 +17,11 @@ Differences, all deliberate:
   kernels do not take, raise instead of silently running the fp32 reference
   (the oracle lives outside the product, under ``oracle/``);
 * the quantised path supports split-K as well;
-* ``config=None`` picks split-K from the MI355X occupancy heuristic
-  (:func:`flashattntile_amd.autotune.decode_split_k`) instead of an L4-tuned
-  JSON store; an explicit ``split_k`` is honoured exactly;
+* ``config=None`` takes the launch stored for this shape in the gfx950
+  tuned-config store (:func:`flashattntile_amd.autotune.best_config`, keyed by
+  :func:`~flashattntile_amd.autotune.decode_signature`) and otherwise the
+  MI355X partition heuristic (:func:`~flashattntile_amd.autotune.decode_partition`);
+  an explicit ``split_k`` is honoured exactly;
 * validation costs one device->host synchronisation instead of ~6.
 
 :func:`paged_decode_launch` is the sync-free entry below the validation, for
@@ -28,10 +30,12 @@ callers (benchmarks, CUDA-graph-style capture loops) that validated once.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from .. import _hip
-from ..autotune import decode_partition
+from ..autotune import best_config, decode_partition, decode_signature
 from ..paging import PagedKVCache, _check_layout, cache_stats
 
 __all__ = [
@@ -40,6 +44,7 @@ __all__ = [
     "paged_decode_attention_fp8",
     "paged_decode_attention_multi",
     "paged_decode_launch",
+    "resolve_decode_config",
 ]
 
 # split_k None -> MI355X partition heuristic (split_k and pages_per_split from
@@ -49,20 +54,51 @@ __all__ = [
 # library choose from the grid size); num_stages is accepted for signature
 # compatibility with the reference's Triton knob and validated the same way,
 # but the HIP kernel's pipeline depth is fixed (one 16-token unit prefetched
-# per wave).
-DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2, "pages_per_split": None}
+# per wave).  kernel None lets the library choose the kernel family; "valu"
+# or "mfma" forces one (what a tuning run stores for its shape).
+DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2, "pages_per_split": None, "kernel": None}
+
+_KERNEL_CODES = {None: _hip.KERNEL_AUTO, "valu": _hip.KERNEL_DECODE_VALU, "mfma": _hip.KERNEL_DECODE_MFMA}
 
 _QUANT_DTYPES = tuple(d for d in (torch.int8, getattr(torch, "float8_e4m3fn", None)) if d is not None)
 
 
 def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, max_len: int,
                     total_pages: int, q_len: int = 1) -> dict:
+    """``decode.py:474-500``: an explicit config, else the stored winner for
+    this shape, else the heuristic.  A stored entry the checks below reject
+    is ignored with a warning.  Needs no device synchronisation."""
+    if config is None:
+        sig = decode_signature(int(q.shape[0]), int(q.shape[-2]), cache.num_kv_heads, cache.head_dim,
+                               cache.page_size, max_len, total_pages, cache.k_cache.dtype, q_len)
+        stored = best_config("decode", sig)
+        if stored:
+            try:
+                return _merge_config({k: v for k, v in stored.items() if k in DEFAULT_CONFIG}, q, cache, max_len,
+                                     total_pages, q_len)
+            except ValueError as exc:
+                warnings.warn(f"ignoring the stored decode config for {sig}: {exc}", RuntimeWarning, stacklevel=3)
+        return _merge_config({}, q, cache, max_len, total_pages, q_len)
+    unknown = set(config) - set(DEFAULT_CONFIG)
+    if unknown:
+        raise ValueError(f"unknown decode config keys: {sorted(unknown)}")
+    return _merge_config(config, q, cache, max_len, total_pages, q_len)
+
+
+def resolve_decode_config(q: torch.Tensor, cache: PagedKVCache, max_len: int, total_pages: int,
+                          config: dict | None = None, q_len: int = 1) -> dict:
+    """The launch the decode wrappers make for these inputs: ``config`` if
+    given, else the stored winner for the shape, else the heuristic.  Host
+    work only; ``max_len`` and ``total_pages`` are the batch's longest
+    sequence and its page count.  For callers of :func:`paged_decode_launch`
+    (benchmarks, capture loops) that validated once."""
+    return _resolve_config(config, q, cache, max_len, total_pages, q_len)
+
+
+def _merge_config(config: dict, q: torch.Tensor, cache: PagedKVCache, max_len: int, total_pages: int,
+                  q_len: int) -> dict:
     resolved = dict(DEFAULT_CONFIG)
-    if config is not None:
-        unknown = set(config) - set(DEFAULT_CONFIG)
-        if unknown:
-            raise ValueError(f"unknown decode config keys: {sorted(unknown)}")
-        resolved.update(config)
+    resolved.update(config)
     if resolved["split_k"] is None:
         max_pages = -(-max_len // cache.page_size)
         split, chunk = decode_partition(int(q.shape[0]), int(q.shape[-2]), cache.num_kv_heads, max_pages,
@@ -86,6 +122,10 @@ def _resolve_config(config: dict | None, q: torch.Tensor, cache: PagedKVCache, m
         raise ValueError(f"num_warps must be 4 or 8 waves per workgroup on MI355X, got {resolved['num_warps']}")
     if resolved["num_stages"] < 1:
         raise ValueError(f"num_stages must be >= 1, got {resolved['num_stages']}")
+    if resolved["kernel"] not in _KERNEL_CODES:
+        raise ValueError(f"kernel must be None, 'valu' or 'mfma', got {resolved['kernel']!r}")
+    if resolved["kernel"] == "valu" and q_len > 1:
+        raise ValueError("kernel 'valu' takes one query per sequence; multi-token decode runs on 'mfma'")
     return resolved
 
 
@@ -151,13 +191,15 @@ def paged_decode_launch(
     scales=None,
     waves_per_group: int | None = None,
     pages_per_split: int = 0,
+    kernel: str | None = None,
 ) -> torch.Tensor:
     """Enqueue the HIP decode without validation or synchronisation.
 
     ``q`` (``[B, H, D]``, or ``[B, T, H, D]`` for multi-token decode) must be
     contiguous fp16/bf16 on the cache's device; ``out`` (default
     ``empty_like(q)``) and ``workspace`` (default: allocated) may be passed in
-    to avoid allocations.
+    to avoid allocations.  ``kernel``: None (library's choice), ``"valu"`` or
+    ``"mfma"``.
     """
     if cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
         raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
@@ -174,7 +216,7 @@ def paged_decode_launch(
     _hip.paged_decode(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, out,
                       cache.page_size, softmax_scale, split_k, workspace=workspace,
                       k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0,
-                      pages_per_split=pages_per_split)
+                      pages_per_split=pages_per_split, kernel=_KERNEL_CODES[kernel])
     return out
 
 
@@ -205,7 +247,7 @@ def paged_decode_attention(
     if cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"],
-                               pages_per_split=cfg["pages_per_split"])
+                               pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"])
 
 
 def paged_decode_attention_fp8(
@@ -241,7 +283,8 @@ def paged_decode_attention_fp8(
         raise ValueError("scales must be float32")
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"],
                                scales={"k": k_scale.contiguous(), "v": v_scale.contiguous()},
-                               waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"])
+                               waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"],
+                               kernel=cfg["kernel"])
 
 
 def paged_decode_attention_multi(
@@ -286,4 +329,5 @@ def paged_decode_attention_multi(
     elif cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], scales=sc,
-                               pages_per_split=cfg["pages_per_split"])
+                               waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"],
+                               kernel=cfg["kernel"])

@@ -4,9 +4,13 @@ Keeps the reference signature, config keys and validation
 (``flashattn_tile/kernels/prefill.py:145-326``).  The HIP kernel runs QK^T
 and PV on CDNA4 MFMA (v_mfma_f32_32x32x16_{f16,bf16}) with fp32
 accumulation; the Triton tile knobs (BLOCK_M/BLOCK_N/num_warps/num_stages)
-are validated as in the reference but the gfx950 kernel uses its own fixed
-tiling.  There is no CPU fallback: non-ROCm tensors or a dtype other than
-fp16/bf16 raise.
+are validated as in the reference but the gfx950 kernels use their own fixed
+tiling.  The one gfx950 knob is ``kernel``: ``"pingpong"`` (8 waves, 256 query
+rows per workgroup), ``"4wave"`` (128 rows) or None (chosen from the grid
+size).  With ``config=None`` the stored winner for the shape is used
+(:func:`flashattntile_amd.autotune.best_config`, the reference's lookup at
+``prefill.py:167-191``).  There is no CPU fallback: non-ROCm tensors or a
+dtype other than fp16/bf16 raise.
 
 ``paged_prefill_attention`` is the paged (chunked) form the reference lacks:
 the queries of each sequence attend to that sequence's keys in a
@@ -19,21 +23,33 @@ from __future__ import annotations
 import torch
 
 from .. import _hip
+from ..autotune import best_config, prefill_paged_signature, prefill_signature
 from ..paging import PagedKVCache, _check_layout
 
 __all__ = ["DEFAULT_CONFIG", "prefill_attention", "prefill_launch", "paged_prefill_attention",
            "paged_prefill_launch"]
 
-DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3}
+DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3, "kernel": None}
+
+_KERNEL_CODES = {None: _hip.KERNEL_AUTO, "pingpong": _hip.KERNEL_PREFILL_PINGPONG,
+                 "4wave": _hip.KERNEL_PREFILL_4WAVE}
 
 
-def _resolve_config(config: dict | None) -> dict:
+def _resolve_config(config: dict | None, kind: str | None = None, signature: str | None = None) -> dict:
+    """``prefill.py:167-191``: an explicit config, else the stored winner for
+    ``kind:signature`` (when given), else the defaults."""
     resolved = dict(DEFAULT_CONFIG)
-    if config is not None:
+    if config is None:
+        stored = best_config(kind, signature) if kind and signature else None
+        if stored and stored.get("kernel", None) in _KERNEL_CODES:
+            resolved["kernel"] = stored.get("kernel")
+    else:
         unknown = set(config) - set(DEFAULT_CONFIG)
         if unknown:
             raise ValueError(f"unknown prefill config keys: {sorted(unknown)}")
         resolved.update(config)
+    if resolved["kernel"] not in _KERNEL_CODES:
+        raise ValueError(f"kernel must be None, 'pingpong' or '4wave', got {resolved['kernel']!r}")
     for key in ("BLOCK_M", "BLOCK_N"):
         val = resolved[key]
         if val <= 0 or val & (val - 1):
@@ -110,11 +126,13 @@ def prefill_launch(
     softmax_scale: float,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    kernel: str | None = None,
 ) -> torch.Tensor:
     """Enqueue the HIP prefill without validation or synchronisation.
 
     ``q``/``k``/``v`` must have a contiguous head_dim axis; ``max_seqlen_*``
-    must bound every sequence (they size the launch grid).
+    must bound every sequence (they size the launch grid).  ``kernel``:
+    None (library's choice), ``"pingpong"`` or ``"4wave"``.
     """
     if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("q, k, v need a contiguous head_dim axis")
@@ -124,7 +142,7 @@ def prefill_launch(
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     _hip.prefill_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k,
-                        causal, softmax_scale, workspace=workspace)
+                        causal, softmax_scale, workspace=workspace, kernel=_KERNEL_CODES[kernel])
     return out
 
 
@@ -159,7 +177,9 @@ def prefill_attention(
         raise ValueError(f"max_seqlen_q {max_seqlen_q} is smaller than the longest query sequence {longest_q}")
     if max_seqlen_k < longest_k:
         raise ValueError(f"max_seqlen_k {max_seqlen_k} is smaller than the longest key sequence {longest_k}")
-    _resolve_config(config)
+    sig = prefill_signature(cu_seqlens_q.shape[0] - 1, q.shape[1], k.shape[1], q.shape[2], int(max_seqlen_q),
+                            int(max_seqlen_k), causal)
+    cfg = _resolve_config(config, "prefill", sig)
     if not all(t.is_cuda for t in (q, k, v, cu_seqlens_q, cu_seqlens_k)):
         raise RuntimeError("prefill_attention: inputs must be ROCm device tensors; this build runs the gfx950 "
                            "HIP kernel only (no CPU or reference fallback)")
@@ -169,7 +189,7 @@ def prefill_attention(
     k = k if k.stride(-1) == 1 else k.contiguous()
     v = v if v.stride(-1) == 1 else v.contiguous()
     return prefill_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
-                          bool(causal), scale)
+                          bool(causal), scale, kernel=cfg["kernel"])
 
 
 def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
@@ -233,8 +253,10 @@ def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
 
 
 def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: torch.Tensor, max_seqlen_q: int,
-                         causal: bool, softmax_scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Enqueue ``fat_prefill_paged`` without validation or synchronisation."""
+                         causal: bool, softmax_scale: float, out: torch.Tensor | None = None,
+                         kernel: str | None = None) -> torch.Tensor:
+    """Enqueue ``fat_prefill_paged`` without validation or synchronisation
+    (``kernel`` as for :func:`prefill_launch`)."""
     if q.stride(-1) != 1 or cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
         raise ValueError("q and the cache need a contiguous head_dim axis")
     if out is None:
@@ -242,7 +264,7 @@ def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: tor
     pt = cache.page_table if cache.page_table.stride(-1) == 1 else cache.page_table.contiguous()
     sl = cache.seq_lens if cache.seq_lens.is_contiguous() else cache.seq_lens.contiguous()
     _hip.prefill_paged(q, cache.k_cache, cache.v_cache, pt, sl, cu_seqlens_q, out, cache.page_size,
-                       int(max_seqlen_q), bool(causal), float(softmax_scale))
+                       int(max_seqlen_q), bool(causal), float(softmax_scale), kernel=_KERNEL_CODES[kernel])
     return out
 
 
@@ -253,13 +275,16 @@ def paged_prefill_attention(
     max_seqlen_q: int,
     causal: bool = True,
     softmax_scale: float | None = None,
+    config: dict | None = None,
 ) -> torch.Tensor:
     """Paged (chunked) prefill: ``q`` ``[total_q, num_heads, head_dim]`` packed
     by ``cu_seqlens_q`` (int32 ``[B + 1]``) attends, per sequence b, to keys
     ``0 .. seq_lens[b] - 1`` of ``cache`` (which already holds the chunk's
     own K/V).  Causal masking is bottom-right aligned, as in
     :func:`prefill_attention`, so query i of a q_len-token chunk sees keys
-    ``j <= i + seq_lens[b] - q_len``.  Returns ``q``'s shape and dtype.
+    ``j <= i + seq_lens[b] - q_len``.  ``config`` as for
+    :func:`prefill_attention` (store kind ``prefill_paged``).  Returns
+    ``q``'s shape and dtype.
     """
     longest_q = _validate_paged(q, cache, cu_seqlens_q, causal)
     if max_seqlen_q <= 0:
@@ -271,6 +296,10 @@ def paged_prefill_attention(
                            "gfx950 HIP kernel only (no CPU or reference fallback)")
     if q.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"paged_prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    sig = prefill_paged_signature(cache.batch_size, q.shape[1], cache.num_kv_heads, cache.head_dim,
+                                  cache.page_size, int(max_seqlen_q), causal)
+    cfg = _resolve_config(config, "prefill_paged", sig)
     scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
     q = q if q.stride(-1) == 1 else q.contiguous()
-    return paged_prefill_launch(q, cache, cu_seqlens_q, int(max_seqlen_q), bool(causal), scale)
+    return paged_prefill_launch(q, cache, cu_seqlens_q, int(max_seqlen_q), bool(causal), scale,
+                                kernel=cfg["kernel"])

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 5
+#define FAT_ABI_VERSION 6
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -52,6 +52,17 @@ enum fat_dtype {
   FAT_DTYPE_I8 = 2,      /* symmetric int8 KV storage (scale = absmax/127) */
   FAT_DTYPE_FP8E4M3 = 3, /* OCP float8 e4m3fn KV storage (absmax/448)      */
   FAT_DTYPE_F32 = 4      /* IEEE binary32 (fat_quantize_pages source only) */
+};
+
+/* Kernel choice (the `kernel` field of the decode and prefill arguments).
+ * FAT_KERNEL_AUTO lets the library choose from the shape; the others force
+ * one kernel family, e.g. the winner a tuning run stored for this shape. */
+enum fat_kernel {
+  FAT_KERNEL_AUTO = 0,
+  FAT_KERNEL_DECODE_VALU = 1,      /* one query per sequence (q_len <= 1)     */
+  FAT_KERNEL_DECODE_MFMA = 2,      /* any cache dtype and q_len               */
+  FAT_KERNEL_PREFILL_PINGPONG = 1, /* 8 waves, 256 query rows per workgroup   */
+  FAT_KERNEL_PREFILL_4WAVE = 2     /* 4 waves, 128 query rows per workgroup   */
 };
 
 /* Error codes. */
@@ -129,6 +140,7 @@ typedef struct fat_decode_args {
    * batch * q_len, ...).  At most 64 tokens. */
   int64_t q_stride_t, out_stride_t;
   int32_t q_len;
+  int32_t kernel; /* FAT_KERNEL_AUTO, _DECODE_VALU or _DECODE_MFMA */
 } fat_decode_args;
 
 /*
@@ -140,8 +152,8 @@ typedef struct fat_decode_args {
  *   out [total_q, num_heads, head_dim]      dtype
  * Causal masking is bottom-right aligned: query i of a sequence sees key j
  * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
- * The kernel needs a workspace of fat_prefill_workspace_bytes(total_k,
- * num_kv_heads, head_dim) bytes, used to stage V in key-major order.
+ * fat_prefill_workspace_bytes() returns 0: the kernels need no workspace
+ * (V is read key-major and transposed in LDS), so `workspace` may be NULL.
  */
 typedef struct fat_prefill_args {
   const void* q;
@@ -166,6 +178,7 @@ typedef struct fat_prefill_args {
   int32_t causal;
   int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
   float softmax_scale;
+  int32_t kernel; /* FAT_KERNEL_AUTO, _PREFILL_PINGPONG or _PREFILL_4WAVE */
 } fat_prefill_args;
 
 /*
@@ -210,6 +223,7 @@ typedef struct fat_prefill_paged_args {
   int32_t causal;
   int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
   float softmax_scale;
+  int32_t kernel; /* FAT_KERNEL_AUTO, _PREFILL_PINGPONG or _PREFILL_4WAVE */
 } fat_prefill_paged_args;
 
 /*

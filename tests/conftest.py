@@ -2,10 +2,16 @@
 
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
 import pytest
+
+# config=None launches use the library's heuristics, not the committed tuned
+# store: a stored `kernel` would override the kernel-forcing fixtures.  The
+# store tests point FAT_TUNED_CONFIGS at a file of their own.
+os.environ["FAT_TUNED_CONFIGS"] = "none"
 
 ROOT = Path(__file__).resolve().parents[1]
 for p in (ROOT, ROOT / "tests"):

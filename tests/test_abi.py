@@ -51,6 +51,7 @@ def test_struct_layout_matches_ctypes(tmp_path):
     fields = {
         "fat_decode_args": [f for f, _ in _hip.DecodeArgs._fields_],
         "fat_prefill_args": [f for f, _ in _hip.PrefillArgs._fields_],
+        "fat_prefill_paged_args": [f for f, _ in _hip.PrefillPagedArgs._fields_],
         "fat_quantize_args": [f for f, _ in _hip.QuantizeArgs._fields_],
         "fat_append_args": [f for f, _ in _hip.AppendArgs._fields_],
     }
@@ -68,6 +69,7 @@ def test_struct_layout_matches_ctypes(tmp_path):
         struct, name, val = line.split()
         got[(struct, name)] = int(val)
     for struct, cls in (("fat_decode_args", _hip.DecodeArgs), ("fat_prefill_args", _hip.PrefillArgs),
+                        ("fat_prefill_paged_args", _hip.PrefillPagedArgs),
                         ("fat_quantize_args", _hip.QuantizeArgs), ("fat_append_args", _hip.AppendArgs)):
         assert got[(struct, "size")] == ctypes.sizeof(cls)
         for n, _ in cls._fields_:
@@ -110,6 +112,11 @@ def test_decode_argument_errors_are_reported():
     a.q_dtype = 9
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "q_dtype" in _err()
     a.q_dtype = _hip.DT_F16
+    a.kernel = 3
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "kernel" in _err()
+    a.kernel, a.q_len = _hip.KERNEL_DECODE_VALU, 2
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "VALU" in _err()
+    a.kernel, a.q_len = _hip.KERNEL_AUTO, 0
     a.k_stride_slot = 3  # 6-byte rows: misaligned for 16-byte loads
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "aligned" in _err()
 
@@ -120,6 +127,18 @@ def test_prefill_argument_errors_are_reported():
     a = _hip.PrefillArgs()
     assert lib.fat_prefill_varlen(ctypes.byref(a), None) != 0
     assert _err()
+    for f in ("q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "out"):
+        setattr(a, f, 0x1000)
+    a.batch, a.num_heads, a.num_kv_heads, a.head_dim, a.dtype = 1, 4, 2, 128, _hip.DT_F16
+    a.kernel = 3
+    assert lib.fat_prefill_varlen(ctypes.byref(a), None) == 1 and "kernel" in _err()
+    p = _hip.PrefillPagedArgs()
+    for f in ("q", "k_cache", "v_cache", "page_table", "seq_lens", "cu_seqlens_q", "out"):
+        setattr(p, f, 0x1000)
+    p.batch, p.num_heads, p.num_kv_heads, p.head_dim, p.dtype, p.page_size = 1, 4, 2, 128, _hip.DT_F16, 16
+    p.num_pages, p.max_pages = 1, 1
+    p.kernel = -1
+    assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "kernel" in _err()
 
 
 def test_quantize_argument_errors_are_reported():

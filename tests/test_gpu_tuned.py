@@ -1,0 +1,132 @@
+"""GPU tests of the per-launch kernel choice (ABI field ``kernel``) and of
+the gfx950 tuned-config store routing ``config=None`` launches.
+
+A launch forced through the config is the same launch as one forced through
+the environment variables the other GPU tests use, so its output must be
+bit-identical; a launch taken from the store must be bit-identical to the
+same config passed explicitly.  Parity against the fp32 oracle (2e-3,
+tests/_parity.py) is checked once per kernel.
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+from _parity import assert_parity, make_paged, make_query, make_varlen
+from flashattntile_amd import (PagedKVCache, paged_decode_attention, paged_decode_attention_multi,
+                               paged_prefill_attention, prefill_attention)
+from flashattntile_amd import autotune as at
+from oracle.reference import ref_attention_paged, ref_attention_varlen
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+LENS = [1, 17, 255, 1000, 4096]
+
+
+def _decode_case(lens, h, hk, dtype, seed):
+    k, v, pt, sl = make_paged(lens, hk, 128, 16, dtype, seed=seed, device=DEV)
+    return make_query(len(lens), h, 128, dtype, seed=seed + 1, device=DEV), PagedKVCache(k, v, pt, sl, 16)
+
+
+@pytest.mark.parametrize("kern", ["valu", "mfma"])
+@pytest.mark.parametrize("h,hk", [(32, 8), (8, 2), (32, 1)])
+def test_decode_kernel_config_equals_env_forcing(kern, h, hk, monkeypatch):
+    label = f"decode kernel={kern} H{h}/{hk}"
+    print(label, flush=True)
+    q, cache = _decode_case(LENS, h, hk, torch.bfloat16, seed=h + hk)
+    out_cfg = paged_decode_attention(q, cache, config={"split_k": 4, "kernel": kern})
+    monkeypatch.setenv("FAT_DECODE_KERNEL", "mfma" if kern == "valu" else "valu")  # the field wins over it
+    out_cfg2 = paged_decode_attention(q, cache, config={"split_k": 4, "kernel": kern})
+    monkeypatch.setenv("FAT_DECODE_KERNEL", kern)
+    out_env = paged_decode_attention(q, cache, config={"split_k": 4})
+    torch.cuda.synchronize()
+    assert torch.equal(out_cfg, out_env) and torch.equal(out_cfg2, out_env), label
+    ref = ref_attention_paged(q.cpu(), cache.k_cache.cpu(), cache.v_cache.cpu(), cache.page_table.cpu(),
+                              cache.seq_lens.cpu(), return_fp32=True)
+    assert_parity(out_cfg, ref, label=label)
+
+
+def test_multi_token_decode_kernel_choice():
+    print("multi-token decode kernel choice", flush=True)
+    k, v, pt, sl = make_paged([40, 300], 8, 128, 16, torch.float16, seed=3, device=DEV)
+    cache = PagedKVCache(k, v, pt, sl, 16)
+    q = torch.randn(2, 3, 32, 128, generator=torch.Generator().manual_seed(4)).half().to(DEV)
+    a = paged_decode_attention_multi(q, cache, config={"split_k": 2, "kernel": "mfma"})
+    b = paged_decode_attention_multi(q, cache, config={"split_k": 2})
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="one query per sequence"):
+        paged_decode_attention_multi(q, cache, config={"split_k": 2, "kernel": "valu"})
+
+
+@pytest.mark.parametrize("kern", ["pingpong", "4wave"])
+def test_prefill_kernel_config_equals_env_forcing(kern, monkeypatch):
+    label = f"prefill kernel={kern}"
+    print(label, flush=True)
+    lens = [1, 255, 1000]
+    q, k, v, cu = make_varlen(lens, 32, 8, 128, torch.float16, seed=11, device=DEV)
+    out_cfg = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True, config={"kernel": kern})
+    monkeypatch.setenv("FAT_PREFILL_KERNEL", kern)
+    out_env = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_cfg, out_env), label
+    ref = ref_attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), causal=True, return_fp32=True)
+    assert_parity(out_cfg, ref, label=label)
+    # the paged prefill takes the same knob
+    kc, vc, pt, sl = make_paged(lens, 8, 128, 16, torch.float16, seed=12, device=DEV)
+    cache = PagedKVCache(kc, vc, pt, sl, 16)
+    p_cfg = paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
+    monkeypatch.setenv("FAT_PREFILL_KERNEL", "4wave" if kern == "pingpong" else "pingpong")
+    p_cfg2 = paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
+    monkeypatch.setenv("FAT_PREFILL_KERNEL", kern)
+    p_env = paged_prefill_attention(q, cache, cu, max(lens))
+    torch.cuda.synchronize()
+    assert torch.equal(p_cfg, p_env) and torch.equal(p_cfg2, p_env), label
+
+
+def test_store_routes_config_none_launches(tmp_path, monkeypatch):
+    print("tuned store routes config=None launches", flush=True)
+    path = tmp_path / "store.json"
+    monkeypatch.setenv("FAT_TUNED_CONFIGS", str(path))
+    q, cache = _decode_case(LENS, 32, 8, torch.float16, seed=21)
+    total = sum(-(-n // 16) for n in LENS)
+    sig = at.decode_signature(len(LENS), 32, 8, 128, 16, max(LENS), total, torch.float16)
+    for cfg in ({"split_k": 3, "pages_per_split": 0, "num_warps": 8, "kernel": "mfma"},
+                {"split_k": 5, "pages_per_split": 16, "num_warps": 4, "kernel": "valu"}):
+        at.save_best("decode", sig, cfg)
+        got = paged_decode_attention(q, cache)
+        want = paged_decode_attention(q, cache, config=dict(cfg))
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), cfg
+    lens = [1, 255, 1000]
+    qp, k, v, cu = make_varlen(lens, 32, 8, 128, torch.bfloat16, seed=22, device=DEV)
+    psig = at.prefill_signature(3, 32, 8, 128, 1000, 1000, True)
+    for kern in ("pingpong", "4wave"):
+        at.save_best("prefill", psig, {"kernel": kern})
+        got = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True)
+        want = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True, config={"kernel": kern})
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), kern
+
+
+def test_committed_store_entry_runs(monkeypatch):
+    """A committed decode entry (B8 ctx1024 fp16, from a tuning run on
+    MI355X) routes config=None to its stored launch, which passes parity."""
+    data = json.loads(at.TUNED_CONFIGS_PATH.read_text())
+    sig = "B8_H32_Hkv8_D128_P16_L1024_fp16"
+    entry = data["configs"].get(f"decode:{sig}")
+    if entry is None:
+        pytest.skip("no tuned entry for B8 ctx1024 in the committed store")
+    print(f"committed store entry {sig} {entry['config']}", flush=True)
+    monkeypatch.setenv("FAT_TUNED_CONFIGS", str(at.TUNED_CONFIGS_PATH))
+    q, cache = _decode_case([1024] * 8, 32, 8, torch.float16, seed=31)
+    got = paged_decode_attention(q, cache)
+    want = paged_decode_attention(q, cache, config=dict(entry["config"]))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ref = ref_attention_paged(q.cpu(), cache.k_cache.cpu(), cache.v_cache.cpu(), cache.page_table.cpu(),
+                              cache.seq_lens.cpu(), return_fp32=True)
+    assert_parity(got, ref, label=f"store {sig}")
