@@ -20,10 +20,13 @@
 //     registers (the key order inside an MFMA k-step is chosen to match the
 //     accumulator layout), and V^T comes from LDS through
 //     ds_read_b64_tr_b16, so V never needs a transposed copy;
-//   * P is rounded to the input dtype for the PV product (as
-//     prefill.py:128 does); for bf16 it is split into hi + lo bf16 parts and
-//     both are multiplied, which keeps the result within fp32-level error of
-//     the fp32 reference;
+//   * P is rounded to fp16 for the PV product (prefill.py:128 rounds it to
+//     the input dtype).  For bf16 inputs the 8-wave kernel stages V as fp16,
+//     each staging wave's rows scaled by a power of two that is 1 unless
+//     some |v| >= 2^15, and folds the scales into P's exponent; the 4-wave
+//     kernel multiplies bf16 V by P split into hi + lo bf16 parts.  Both keep
+//     the result within fp32-level error of the fp32 reference (the first
+//     adds at most max|v| * 2^-39 per V element when |v| reaches 2^15);
 //   * exp is 2^(x * log2 e) on v_exp_f32;
 //   * the 1-D grid walks query blocks longest-first (causal balance) and
 //     assigns the query heads that share a KV head to the same XCD
@@ -561,6 +564,15 @@ void prefill_pp_kernel(const PrefillParams p) {
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * V_RS];
+  // bf16: V tiles are staged as fp16 so that PV runs as one fp16 MFMA with P
+  // rounded to fp16 (relative error 2^-11, as on the fp16 path) instead of
+  // two bf16 MFMAs with P split into hi + lo parts.  Each staging wave scales
+  // its rows by 2^-s (s = 0 unless some |v| >= 2^15), which keeps them inside
+  // fp16's range and exact apart from fp16 subnormals (absolute error
+  // <= 2^-25 * 2^s); vsc[buffer][wave] holds s.  The softmax folds
+  // 2^(s - e_acc) into P's exponent, where O is kept as acc * 2^e_acc.
+  constexpr bool VH = SPLIT_P;
+  __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
   const int per = p.B * p.H;
   const int outer = blockIdx.x / per;
@@ -661,6 +673,45 @@ void prefill_pp_kernel(const PrefillParams p) {
   };
   auto lstore = [&](int buf) {
     if constexpr (PG == 2) pr.mask_tail(stage);
+    if constexpr (VH) {
+      if (grp == 1) {
+        // The wave's largest bf16 exponent field e (inf and NaN: 255); its
+        // rows are scaled by 2^-s, s = max(0, e - 141), so |v| 2^-s < 2^15.
+        u16x2 em = {0, 0};
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            em = __builtin_elementwise_max(em, __builtin_bit_cast(u16x2, stage[u][e] & 0x7f807f80u));
+        const int le = (int)(max(em[0], em[1]) >> 7);
+        int sw = 0;
+        if (__builtin_amdgcn_ballot_w64(le > 141) != 0) {  // rare: some |v| >= 2^15
+          float m = (float)le;
+          m = within_quad<OpMax, 4>(m);
+          m = across_rows<OpMax, 4>(m);
+          sw = __builtin_amdgcn_readfirstlane(max(0, (int)m - 141));
+        }
+        if (sw == 0) {
+#pragma unroll
+          for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const u32 wv = stage[u][e];
+              stage[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv), Pair<BF16>::hi(wv));
+            }
+        } else {
+          const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 114
+#pragma unroll
+          for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const u32 wv = stage[u][e];
+              stage[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv) * f, Pair<BF16>::hi(wv) * f);
+            }
+        }
+        if (lane == 0) vsc[buf][w - 4] = sw;
+      }
+    }
     uint16_t* dst = lds0 + buf * lds_buf + lds_off;
 #pragma unroll
     for (int u = 0; u < LOADS; ++u)
@@ -675,7 +726,7 @@ void prefill_pp_kernel(const PrefillParams p) {
 
   f32x16 s[2];
   u32x4 pf[2][2];
-  u32x4 pl[2][2];
+  int e_acc = 0;  // bf16: O = acc * 2^e_acc
 
   // S(t) = K(t) Q^T into s.
   auto qk = [&](int t) {
@@ -706,8 +757,7 @@ void prefill_pp_kernel(const PrefillParams p) {
           const u32x2 lo = lds_read_tr16(vp);
           const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
           const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
-          acc[db] = Mfma<T>::mma(a, pf[jb][tt], acc[db]);
-          if constexpr (SPLIT_P) acc[db] = Mfma<T>::mma(a, pl[jb][tt], acc[db]);
+          acc[db] = Mfma<F16>::mma(a, pf[jb][tt], acc[db]);  // fp16 V and P (bf16: scaled V)
         }
       }
   };
@@ -744,6 +794,36 @@ void prefill_pp_kernel(const PrefillParams p) {
     // which every p > 2^kLazyPP forces.  P and the fp32 sums hold values up
     // to 2^kLazyPP exactly as well as values up to 1.
     const float cm = POS ? c : 1.f;
+    // bf16: element (tt, e2) of this lane holds a key staged by wave
+    // ((4g + 8(2tt + e2/2)) mod kRowsPerLoad) / (64 / CPR) of group B; its
+    // P is computed as 2^(s c - m + o) with o = s_wave - e_acc <= 0, and its
+    // partial row sum is scaled back by 2^-o.
+    float off[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    float back[2][2] = {{1.f, 1.f}, {1.f, 1.f}};
+    if constexpr (VH) {
+      const u32x4 sc4 = *reinterpret_cast<const u32x4*>(&vsc[t & 1][0]);
+      int sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = __builtin_amdgcn_readfirstlane((int)sc4[i]);
+      const int smax = max(max(sv[0], sv[1]), max(sv[2], sv[3]));
+      if (smax > e_acc) {  // rare: a tile with larger |v| than any before
+        const float down = as_f32((u32)(127 - (smax - e_acc)) << 23);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[db][r] *= down;
+        e_acc = smax;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int wl = ((4 * g + 8 * (2 * tt + hh)) % kRowsPerLoad) / (64 / CPR);
+          const int sws = wl == 0 ? sv[0] : wl == 1 ? sv[1] : wl == 2 ? sv[2] : sv[3];
+          off[tt][hh] = (float)(sws - e_acc);
+          back[tt][hh] = as_f32((u32)(127 + e_acc - sws) << 23);
+        }
+    }
     auto compute_p = [&]() -> float {
       const float nm = -m_run;
       float lsq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // four partial row sums
@@ -753,15 +833,17 @@ void prefill_pp_kernel(const PrefillParams p) {
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int e2 = 0; e2 < 4; ++e2) {
-            const float x0 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2], cm, nm));
-            const float x1 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2 + 1], cm, nm));
-            const u32 hp = Pair<T>::pack(x0, x1);
-            pf[jb][tt][e2] = hp;
-            if constexpr (SPLIT_P) pl[jb][tt][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
+            const float nmo = VH ? nm + off[tt][e2 >> 1] : nm;
+            const float x0 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2], cm, nmo));
+            const float x1 = fast_exp2(__builtin_fmaf(s[jb][8 * tt + 2 * e2 + 1], cm, nmo));
+            pf[jb][tt][e2] = Pair<F16>::pack(x0, x1);
             // fp32 adds, not v_dot2: a dot2 on one wave stalls the other
             // wave's MFMAs (measured on gfx950), undoing the ping-pong overlap.
-            lsq[jb][tt] += x0 + x1;
+            if constexpr (VH) lsq[tt][e2 >> 1] += x0 + x1;
+            else lsq[jb][tt] += x0 + x1;
           }
+      if constexpr (VH)
+        return (lsq[0][0] * back[0][0] + lsq[0][1] * back[0][1]) + (lsq[1][0] * back[1][0] + lsq[1][1] * back[1][1]);
       return (lsq[0][0] + lsq[0][1]) + (lsq[1][0] + lsq[1][1]);
     };
     float ls = 0.f;
@@ -826,7 +908,7 @@ void prefill_pp_kernel(const PrefillParams p) {
       __builtin_amdgcn_s_setprio(2);
       qk(t);
       pv(t - 1);
-      MfmaPhaseOrder<0, 2 * KS + 4 * DB, 2 * KS, SPLIT_P ? 2 : 1, 4>::apply();
+      MfmaPhaseOrder<0, 2 * KS + 4 * DB, 2 * KS, 1, 4>::apply();
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
@@ -845,7 +927,8 @@ void prefill_pp_kernel(const PrefillParams p) {
   }
 
   const float l_tot = xor32<OpAdd>(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if constexpr (VH) inv *= as_f32((u32)(127 + e_acc) << 23);
   if (my_row < q_len) {
     uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
 #pragma unroll

@@ -12,7 +12,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _parity import assert_parity, make_varlen
+from _parity import assert_parity, make_varlen, ulp
 from flashattntile_amd import prefill_attention
 from flashattntile_amd.kernels.prefill import prefill_launch
 from oracle.reference import ref_attention_varlen
@@ -134,3 +134,32 @@ def test_ops_compile_on_device():
     out = torch.compile(fn, fullgraph=True, backend="eager")(q)
     torch.cuda.synchronize()
     assert_parity(out, _ref32(q, k, v, cu, cu, True, scale=0.35), label="compiled prefill op")
+
+
+@pytest.mark.parametrize("huge", [7.0e4, 1.0e6, 3.0e8])
+def test_prefill_bf16_v_beyond_fp16_range(huge, kernel):
+    """bf16 V rows of magnitude >= 2^15 (the 8-wave kernel stages such a
+    staging wave's rows as fp16 scaled by 2^-s and tracks O as acc * 2^e).
+    Key 300 (tile 4) holds huge/8 and the last two keys +-huge, so the scale
+    grows twice along the sequence; queries before key 300 never see a huge
+    row but read rows staged by the same wave (tile 4), which must keep the
+    2e-3 absolute bound; the others are checked relative to their magnitude."""
+    label = f"prefill {kernel} bf16 |v| up to {huge:g}"
+    print(label, flush=True)
+    L = 700
+    q, k, v, cu = make_varlen([L], 8, 2, 128, torch.bfloat16, seed=21)
+    g = torch.Generator().manual_seed(22)
+    for j, f in ((300, huge / 8), (L - 2, -huge), (L - 1, huge)):
+        v[j] = (torch.sign(torch.randn(2, 128, generator=g)) * f).to(torch.bfloat16)
+    q, k, v, cu = q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV)
+    out = prefill_attention(q, k, v, cu, cu, L, L, causal=True)
+    torch.cuda.synchronize()
+    ref = _ref32(q, k, v, cu, cu, True)
+    assert_parity(out[:300], ref[:300], label=f"{label} (queries that see no huge row)")
+    # 2e-3 relative to each output row's magnitude, beyond the final rounding
+    o32, r32 = out[300:].float().cpu(), ref[300:].float()
+    scale = r32.abs().amax(dim=-1, keepdim=True).clamp_min(1.0)
+    rounding = 0.5 * ulp(torch.maximum(o32.abs(), r32.abs()), torch.bfloat16)
+    excess = ((o32 - r32).abs() - rounding) / scale
+    print(f"{label}: max relative error beyond rounding {excess.max().item():.3e}", flush=True)
+    assert torch.isfinite(o32).all() and excess.max().item() <= 2e-3, label
