@@ -18,8 +18,8 @@ __version__ = "0.1.0"
 from . import ops as _ops  # noqa: F401  (registers the custom ops)
 from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8, paged_decode_attention_multi
 from .kernels.prefill import paged_prefill_attention, prefill_attention
-from .ops import (PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, PREFILL_PAGED_OP, paged_decode,
-                  paged_decode_quant, prefill_paged, prefill_varlen)
+from .ops import (PAGED_DECODE_MULTI_OP, PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, PREFILL_PAGED_OP,
+                  paged_decode, paged_decode_multi, paged_decode_quant, prefill_paged, prefill_varlen)
 from .paging import PagedKVCache, allocate, append_tokens, gather_contiguous, gather_paged, validate_cache
 from .quant import QuantScales, dequantize_cache, kv_bytes_per_token, quantize_cache
 
@@ -29,10 +29,12 @@ __all__ = [
     "PREFILL_OP",
     "PAGED_DECODE_QUANT_OP",
     "PREFILL_PAGED_OP",
+    "PAGED_DECODE_MULTI_OP",
     "paged_decode",
     "prefill_varlen",
     "paged_decode_quant",
     "prefill_paged",
+    "paged_decode_multi",
     "paged_prefill_attention",
     "paged_decode_attention",
     "paged_decode_attention_fp8",

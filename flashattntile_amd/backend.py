@@ -15,6 +15,11 @@ Two extension fields the reference backend lacks:
 * ``paged_prefill``: prefill reads K/V from ``kv_cache`` through the page
   table (chunked prefill; the chunk's own K/V already appended) instead of
   from the packed ``k``/``v`` the reference requires (``backend.py:158-162``).
+
+and one extension of the decode route: a ``[batch, q_len, heads, head_dim]``
+query with ``q_len > 1`` (speculative verification, the tokens' K/V already
+appended) runs multi-token decode; ``q_len == 1`` is squeezed as in the
+reference.
 """
 
 from __future__ import annotations
@@ -23,7 +28,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
+from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8, paged_decode_attention_multi
 from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .paging import PagedKVCache, allocate
 
@@ -109,6 +114,11 @@ class FlashAttnTileBackend:
         meta = attn_metadata
         cache = self._resolve_cache(kv_cache, meta)
         if not meta.is_prefill and query.dim() == 4:
+            if query.shape[1] > 1:
+                if query.shape[2] != self.num_heads:
+                    raise ValueError(f"query has {query.shape[2]} heads, backend expects {self.num_heads}")
+                return paged_decode_attention_multi(query, cache, softmax_scale=meta.softmax_scale,
+                                                    scales=meta.kv_scales)
             query = query.squeeze(1)
         if query.dim() != 3:
             raise ValueError(f"query must be 3-D, got {tuple(query.shape)}")

@@ -156,6 +156,82 @@ struct PagedRowsU {
   }
 };
 
+// bf16 V rows held by this wave (LOADS 16-byte chunks per lane) -> fp16,
+// scaled by 2^-s with s = max(0, e - 141) for the wave's largest bf16
+// exponent field e (inf / NaN: 255), so every |v| 2^-s < 2^15 is exact in
+// fp16 up to fp16 subnormals.  Returns s (wave-uniform; 0 unless some
+// |v| >= 2^15).
+template <int LOADS>
+__device__ __forceinline__ int bf16_to_f16_scaled(u32x4 (&reg)[LOADS]) {
+  u16x2 em = {0, 0};
+#pragma unroll
+  for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) em = __builtin_elementwise_max(em, __builtin_bit_cast(u16x2, reg[u][e] & 0x7f807f80u));
+  const int le = (int)(max(em[0], em[1]) >> 7);
+  int sw = 0;
+  if (__builtin_amdgcn_ballot_w64(le > 141) != 0) {  // rare: some |v| >= 2^15
+    float m = (float)le;
+    m = within_quad<OpMax, 4>(m);
+    m = across_rows<OpMax, 4>(m);
+    sw = __builtin_amdgcn_readfirstlane(max(0, (int)m - 141));
+  }
+  if (sw == 0) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const u32 wv = reg[u][e];
+        reg[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv), Pair<BF16>::hi(wv));
+      }
+  } else {
+    const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 114
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const u32 wv = reg[u][e];
+        reg[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv) * f, Pair<BF16>::hi(wv) * f);
+      }
+  }
+  return sw;
+}
+
+// For the V tile whose staging waves wrote their scales to sc[0..3]: moves
+// O = acc * 2^e_acc to the tile's largest scale if that is larger (rare),
+// then gives each (k-step tt, element half hh) of this lane its exponent
+// offset o = s_wave - e_acc <= 0 and the factor 2^-o that scales its
+// partial row sum back.  Element (tt, e2) of a lane in k-group g holds key
+// 4g + 8(2tt + e2/2) + (0..3) of its 32-key block, staged by wave
+// (key mod (256/CPR)) / (64/CPR).
+template <int CPR, int DB>
+__device__ __forceinline__ void v_scale_offsets(const int* sc, int g, int& e_acc, f32x16 (&acc)[DB],
+                                                float (&off)[2][2], float (&back)[2][2]) {
+  const u32x4 sc4 = *reinterpret_cast<const u32x4*>(sc);
+  int sv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sv[i] = __builtin_amdgcn_readfirstlane((int)sc4[i]);
+  const int smax = max(max(sv[0], sv[1]), max(sv[2], sv[3]));
+  if (smax > e_acc) {  // rare: a tile with larger |v| than any before
+    const float down = as_f32((u32)(127 - (smax - e_acc)) << 23);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db][r] *= down;
+    e_acc = smax;
+  }
+  constexpr int kRowsPerLoad = 256 / CPR;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int wl = ((4 * g + 8 * (2 * tt + hh)) % kRowsPerLoad) / (64 / CPR);
+      const int sws = wl == 0 ? sv[0] : wl == 1 ? sv[1] : wl == 2 ? sv[2] : sv[3];
+      off[tt][hh] = (float)(sws - e_acc);
+      back[tt][hh] = as_f32((u32)(127 + e_acc - sws) << 23);
+    }
+}
+
 // A row's running max is only moved (and O rescaled) when a tile's max
 // exceeds it by more than this many log2 units; p = 2^(x - m) then stays
 // below 2^kLazy, which fp16/bf16 P and the fp32 sums hold exactly as well.
@@ -175,13 +251,18 @@ void prefill_kernel(const PrefillParams p) {
   constexpr int V_RS = D + 32;      // spread 16-byte / transposed reads over banks
   constexpr int CPR = D / 8;        // 16-byte chunks per K/V row
   constexpr int LOADS = kBN * CPR / 256;
-  constexpr bool SPLIT_P = std::is_same<T, BF16>::value;
   static_assert(LOADS >= 1, "tile too small");
 
   // Two K/V buffers: tile t+1 is written while tile t is read, so one
   // workgroup barrier per tile suffices.
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * V_RS];
+  // bf16: V is staged as fp16, each wave's rows scaled by 2^-s (s = 0 unless
+  // some |v| >= 2^15; vsc[buffer][wave]), and PV runs as one fp16 MFMA; the
+  // softmax folds 2^(s - e_acc) into P and O is kept as acc * 2^e_acc (see
+  // prefill_pp_kernel).
+  constexpr bool VH = std::is_same<T, BF16>::value;
+  __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
   // ---- work item: longest query blocks first; heads sharing a KV head
   // ---- land on the same XCD (consecutive ids go to consecutive XCDs).
@@ -235,6 +316,7 @@ void prefill_kernel(const PrefillParams p) {
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
   float m_run = -INFINITY;  // scaled (log2) units
   float l_run = 0.f;
+  int e_acc = 0;  // bf16: O = acc * 2^e_acc
 
   // K/V prefetch through buffer loads: the sequence's first row (this KV
   // head) is the scalar base and each lane keeps a 32-bit byte offset, so a
@@ -319,8 +401,23 @@ void prefill_kernel(const PrefillParams p) {
       *reinterpret_cast<u32x4*>(&Ks[buf][(cid / CPR) * K_RS + 8 * (cid % CPR)]) = kreg[u];
     }
   };
+  // bf16: vreg is converted (convert_v) as soon as the step that loaded it
+  // has issued its MFMAs, not after the next barrier, so the V loads of the
+  // following tile are not delayed behind the conversion; v_s carries the
+  // scale to lstore_v.
+  int v_s = 0;
+  auto convert_v = [&]() {
+    if constexpr (VH) {
+      if constexpr (PG == 2) vpr.mask_tail(vreg);
+      v_s = bf16_to_f16_scaled<LOADS>(vreg);
+    }
+  };
   auto lstore_v = [&](int buf) {
-    if constexpr (PG == 2) vpr.mask_tail(vreg);
+    if constexpr (VH) {
+      if (lane == 0) vsc[buf][w] = v_s;
+    } else if constexpr (PG == 2) {
+      vpr.mask_tail(vreg);
+    }
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
@@ -364,6 +461,7 @@ void prefill_kernel(const PrefillParams p) {
     gload_k(0);
     gload_v(0);
     lstore_k(0);
+    convert_v();
     lstore_v(0);
     if (n_tiles > 1) {
       gload_k(1);
@@ -373,6 +471,7 @@ void prefill_kernel(const PrefillParams p) {
     if (n_tiles > 2) gload_k(2);
     __syncthreads();
     qk(0, s_cur);
+    if (n_tiles > 1) convert_v();  // V(1)
   }
   // One pipeline step.  HAS_NEXT (compile time) is false only for the last
   // tile, so S(t+1), the exponentials and the PV MFMAs of every other tile
@@ -430,6 +529,11 @@ void prefill_kernel(const PrefillParams p) {
         for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
     }
 
+    // bf16: exponent offsets of the staging waves' V scales for tile t.
+    float off[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    float back[2][2] = {{1.f, 1.f}, {1.f, 1.f}};
+    if constexpr (VH) v_scale_offsets<CPR>(vsc[buf], g, e_acc, acc, off, back);
+
     // ---- S(t+1) on the MFMA pipe, interleaved with P(t) = 2^(s c - m) ----
 #ifdef FAT_PF_PRIO
     __builtin_amdgcn_s_setprio(1);
@@ -438,24 +542,22 @@ void prefill_kernel(const PrefillParams p) {
     if constexpr (HAS_NEXT) qk(buf ^ 1, s_nxt);
     const float cm = POS ? c : 1.f;
     const float nm = -m_run;
-    float ls = 0.f;
+    float lsq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
     u32x4 pf[2][2];
-    u32x4 pl[2][2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-          const float x0 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2], cm, nm));
-          const float x1 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2 + 1], cm, nm));
+          const float nmo = VH ? nm + off[t][e2 >> 1] : nm;
+          const float x0 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2], cm, nmo));
+          const float x1 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2 + 1], cm, nmo));
           // P^T operand: k-step t of key block jb uses accumulator regs 8t..8t+7.
-          const u32 hp = Pair<T>::pack(x0, x1);
-          pf[jb][t][e2] = hp;
-          if constexpr (SPLIT_P) pl[jb][t][e2] = Pair<T>::pack(x0 - Pair<T>::lo(hp), x1 - Pair<T>::hi(hp));
-          ls += x0 + x1;  // fp32 adds: v_dot2 would stall the other wave's MFMAs
+          pf[jb][t][e2] = Pair<F16>::pack(x0, x1);
+          lsq[t][e2 >> 1] += x0 + x1;  // fp32 adds: v_dot2 would stall the other wave's MFMAs
         }
-    l_run += ls;
+    l_run += (lsq[0][0] * back[0][0] + lsq[0][1] * back[0][1]) + (lsq[1][0] * back[1][0] + lsq[1][1] * back[1][1]);
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -469,8 +571,7 @@ void prefill_kernel(const PrefillParams p) {
           const u32x2 lo = lds_read_tr16(vp);
           const u32x2 hi2 = lds_read_tr16(vp + 8 * V_RS);
           const u32x4 a = {lo[0], lo[1], hi2[0], hi2[1]};
-          acc[db] = Mfma<T>::mma(a, pf[jb][t], acc[db]);
-          if constexpr (SPLIT_P) acc[db] = Mfma<T>::mma(a, pl[jb][t], acc[db]);
+          acc[db] = Mfma<F16>::mma(a, pf[jb][t], acc[db]);  // fp16 V and P (bf16: scaled V)
         }
       }
 #ifdef FAT_PF_PRIO
@@ -479,6 +580,7 @@ void prefill_kernel(const PrefillParams p) {
     if constexpr (HAS_NEXT) {
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) s_cur[jb] = s_nxt[jb];
+      if (tile + 2 < n_tiles) convert_v();  // V(t+2), stored by the next step
     }
   };
   for (int tile = 0; tile + 1 < n_tiles; ++tile) step(tile, std::true_type{});
@@ -486,7 +588,8 @@ void prefill_kernel(const PrefillParams p) {
 
   // ---- epilogue: O = O^T / l, lane writes 4 consecutive dims per store ----
   const float l_tot = xor32<OpAdd>(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if constexpr (VH) inv *= as_f32((u32)(127 + e_acc) << 23);
   if (my_row < q_len) {
     uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
 #pragma unroll
@@ -559,7 +662,6 @@ void prefill_pp_kernel(const PrefillParams p) {
   constexpr int CPR = D / 8;
   constexpr int LOADS = kBN * CPR / 256;  // one 256-thread group stages a whole tile
   constexpr int kRowsPerLoad = 256 / CPR;
-  constexpr bool SPLIT_P = std::is_same<T, BF16>::value;
   static_assert(LOADS >= 1, "tile too small");
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
@@ -571,7 +673,7 @@ void prefill_pp_kernel(const PrefillParams p) {
   // fp16's range and exact apart from fp16 subnormals (absolute error
   // <= 2^-25 * 2^s); vsc[buffer][wave] holds s.  The softmax folds
   // 2^(s - e_acc) into P's exponent, where O is kept as acc * 2^e_acc.
-  constexpr bool VH = SPLIT_P;
+  constexpr bool VH = std::is_same<T, BF16>::value;
   __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
   const int per = p.B * p.H;
@@ -675,40 +777,7 @@ void prefill_pp_kernel(const PrefillParams p) {
     if constexpr (PG == 2) pr.mask_tail(stage);
     if constexpr (VH) {
       if (grp == 1) {
-        // The wave's largest bf16 exponent field e (inf and NaN: 255); its
-        // rows are scaled by 2^-s, s = max(0, e - 141), so |v| 2^-s < 2^15.
-        u16x2 em = {0, 0};
-#pragma unroll
-        for (int u = 0; u < LOADS; ++u)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            em = __builtin_elementwise_max(em, __builtin_bit_cast(u16x2, stage[u][e] & 0x7f807f80u));
-        const int le = (int)(max(em[0], em[1]) >> 7);
-        int sw = 0;
-        if (__builtin_amdgcn_ballot_w64(le > 141) != 0) {  // rare: some |v| >= 2^15
-          float m = (float)le;
-          m = within_quad<OpMax, 4>(m);
-          m = across_rows<OpMax, 4>(m);
-          sw = __builtin_amdgcn_readfirstlane(max(0, (int)m - 141));
-        }
-        if (sw == 0) {
-#pragma unroll
-          for (int u = 0; u < LOADS; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const u32 wv = stage[u][e];
-              stage[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv), Pair<BF16>::hi(wv));
-            }
-        } else {
-          const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 114
-#pragma unroll
-          for (int u = 0; u < LOADS; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const u32 wv = stage[u][e];
-              stage[u][e] = Pair<F16>::pack(Pair<BF16>::lo(wv) * f, Pair<BF16>::hi(wv) * f);
-            }
-        }
+        const int sw = bf16_to_f16_scaled<LOADS>(stage);
         if (lane == 0) vsc[buf][w - 4] = sw;
       }
     }
@@ -800,30 +869,7 @@ void prefill_pp_kernel(const PrefillParams p) {
     // partial row sum is scaled back by 2^-o.
     float off[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
     float back[2][2] = {{1.f, 1.f}, {1.f, 1.f}};
-    if constexpr (VH) {
-      const u32x4 sc4 = *reinterpret_cast<const u32x4*>(&vsc[t & 1][0]);
-      int sv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = __builtin_amdgcn_readfirstlane((int)sc4[i]);
-      const int smax = max(max(sv[0], sv[1]), max(sv[2], sv[3]));
-      if (smax > e_acc) {  // rare: a tile with larger |v| than any before
-        const float down = as_f32((u32)(127 - (smax - e_acc)) << 23);
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[db][r] *= down;
-        e_acc = smax;
-      }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int wl = ((4 * g + 8 * (2 * tt + hh)) % kRowsPerLoad) / (64 / CPR);
-          const int sws = wl == 0 ? sv[0] : wl == 1 ? sv[1] : wl == 2 ? sv[2] : sv[3];
-          off[tt][hh] = (float)(sws - e_acc);
-          back[tt][hh] = as_f32((u32)(127 + e_acc - sws) << 23);
-        }
-    }
+    if constexpr (VH) v_scale_offsets<CPR>(vsc[t & 1], g, e_acc, acc, off, back);
     auto compute_p = [&]() -> float {
       const float nm = -m_run;
       float lsq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // four partial row sums

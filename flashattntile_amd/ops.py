@@ -11,8 +11,8 @@ Same namespace, names and schemas as ``flashattn_tile/ops.py:35-122``:
     SymInt max_seqlen_q, SymInt max_seqlen_k, bool causal,
     float softmax_scale) -> Tensor``
 
-plus two extensions the reference lacks (its quantised decode had no op,
-and its prefill needs packed K/V):
+plus three extensions the reference lacks (its quantised decode had no op,
+its prefill needs packed K/V, and its decode takes one query):
 
 ``flashattn_tile::paged_decode_quant``
     ``(Tensor q, Tensor k_cache, Tensor v_cache, Tensor k_scale,
@@ -22,6 +22,12 @@ and its prefill needs packed K/V):
     ``(Tensor q, Tensor k_cache, Tensor v_cache, Tensor page_table,
     Tensor seq_lens, Tensor cu_seqlens_q, SymInt max_seqlen_q,
     SymInt page_size, bool causal, float softmax_scale) -> Tensor``
+``flashattn_tile::paged_decode_multi``
+    ``(Tensor q, Tensor k_cache, Tensor v_cache, Tensor page_table,
+    Tensor seq_lens, SymInt page_size, float softmax_scale, SymInt split_k,
+    Tensor? k_scale=None, Tensor? v_scale=None) -> Tensor`` -- multi-token
+    (speculative) decode, q ``[batch, q_len, heads, head_dim]``; the
+    reference's decode takes one query per sequence (``decode.py:548-553``).
 
 The real implementations call the gfx950 HIP kernels through the C ABI; the
 fake implementations touch metadata only, so ``torch.compile(fullgraph=True)``
@@ -32,7 +38,7 @@ from __future__ import annotations
 
 import torch
 
-from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8
+from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8, paged_decode_attention_multi
 from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .paging import PagedKVCache
 
@@ -41,17 +47,20 @@ __all__ = [
     "prefill_varlen",
     "paged_decode_quant",
     "prefill_paged",
+    "paged_decode_multi",
     "ops_available",
     "PAGED_DECODE_OP",
     "PREFILL_OP",
     "PAGED_DECODE_QUANT_OP",
     "PREFILL_PAGED_OP",
+    "PAGED_DECODE_MULTI_OP",
 ]
 
 PAGED_DECODE_OP = "flashattn_tile::paged_decode"
 PREFILL_OP = "flashattn_tile::prefill_varlen"
 PAGED_DECODE_QUANT_OP = "flashattn_tile::paged_decode_quant"
 PREFILL_PAGED_OP = "flashattn_tile::prefill_paged"
+PAGED_DECODE_MULTI_OP = "flashattn_tile::paged_decode_multi"
 
 
 @torch.library.custom_op(PAGED_DECODE_OP, mutates_args=())
@@ -168,7 +177,44 @@ def _prefill_paged_fake(q, k_cache, v_cache, page_table, seq_lens, cu_seqlens_q,
     return q.new_empty(q.shape)
 
 
+@torch.library.custom_op(PAGED_DECODE_MULTI_OP, mutates_args=())
+def paged_decode_multi(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    page_size: int,
+    softmax_scale: float,
+    split_k: int,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Multi-token decode: token t of sequence b attends keys
+    ``j <= seq_lens[b] - q_len + t``.  ``split_k`` >= 1 is honoured; 0 takes
+    the library's launch (tuned store, else heuristic).  ``k_scale`` /
+    ``v_scale`` select an int8 / float8_e4m3fn cache."""
+    cache = PagedKVCache(k_cache=k_cache, v_cache=v_cache, page_table=page_table,
+                         seq_lens=seq_lens, page_size=int(page_size))
+    if (k_scale is None) != (v_scale is None):
+        raise ValueError("k_scale and v_scale must be given together")
+    scales = None if k_scale is None else {"k": k_scale, "v": v_scale}
+    config = None if int(split_k) == 0 else {"split_k": int(split_k)}
+    return paged_decode_attention_multi(q, cache, softmax_scale=softmax_scale, config=config, scales=scales)
+
+
+@paged_decode_multi.register_fake
+def _paged_decode_multi_fake(q, k_cache, v_cache, page_table, seq_lens, page_size, softmax_scale, split_k,
+                             k_scale=None, v_scale=None):
+    torch._check(q.dim() == 4, lambda: f"q must be 4-D [batch, q_len, heads, head_dim], got {q.dim()}")
+    torch._check(q.shape[0] == seq_lens.shape[0], lambda: "q batch must match seq_lens")
+    torch._check(q.shape[3] == k_cache.shape[3], lambda: "q head_dim must match cache")
+    torch._check(q.shape[2] % k_cache.shape[2] == 0, lambda: "heads must be divisible by KV heads")
+    return q.new_empty(q.shape)
+
+
 def ops_available() -> bool:
     """True when the custom ops are registered in this process."""
     return all(hasattr(torch.ops.flashattn_tile, name)
-               for name in ("paged_decode", "prefill_varlen", "paged_decode_quant", "prefill_paged"))
+               for name in ("paged_decode", "prefill_varlen", "paged_decode_quant", "prefill_paged",
+                            "paged_decode_multi"))

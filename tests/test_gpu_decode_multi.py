@@ -124,3 +124,32 @@ def test_multi_token_validation():
         paged_decode_attention_multi(q2, cache2, scales={"k": None, "v": None})
     with pytest.raises(ValueError, match="batch, q_len"):
         paged_decode_attention_multi(q2[:, 0], cache2)
+
+
+def test_multi_token_op_compile_and_backend_route():
+    """flashattn_tile::paged_decode_multi (eager, inside torch.compile, and
+    with an int8 cache) and the backend's 4-D decode route give exactly the
+    function's result."""
+    from flashattntile_amd.backend import AttentionMetadata, FlashAttnTileBackend
+
+    print("multi decode op / compile / backend", flush=True)
+    q, cache = _case(LENS, 3, 32, 8, 128, 16, torch.float16, seed=77)
+    want = paged_decode_attention_multi(q, cache, softmax_scale=0.09, config={"split_k": 2})
+    args = (cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, 16, 0.09, 2)
+    got = torch.ops.flashattn_tile.paged_decode_multi(q, *args)
+
+    def fn(x):
+        return torch.ops.flashattn_tile.paged_decode_multi(x, *args)
+
+    got_c = torch.compile(fn, fullgraph=True, backend="eager")(q)
+    backend = FlashAttnTileBackend(num_heads=32, num_kv_heads=8, head_dim=128, page_size=16)
+    got_b = backend.forward(q, cache, AttentionMetadata(softmax_scale=0.09))
+    want_b = paged_decode_attention_multi(q, cache, softmax_scale=0.09)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(got_c, want) and torch.equal(got_b, want_b)
+    qc, sc = quantize_cache(cache, "int8")
+    want_q = paged_decode_attention_multi(q, qc, softmax_scale=0.09, config={"split_k": 2}, scales=sc)
+    got_q = torch.ops.flashattn_tile.paged_decode_multi(q, qc.k_cache, qc.v_cache, qc.page_table, qc.seq_lens, 16,
+                                                        0.09, 2, sc.k, sc.v)
+    torch.cuda.synchronize()
+    assert torch.equal(got_q, want_q)

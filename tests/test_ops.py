@@ -71,6 +71,23 @@ def test_fake_prefill_paged_shapes():
     assert out.shape == (11, 4, 8) and out.device.type == "meta"
 
 
+def test_fake_paged_decode_multi_shapes():
+    with torch._subclasses.fake_tensor.FakeTensorMode():
+        q = torch.empty(3, 4, 8, 16, device="meta")
+        k = torch.empty(12, 16, 2, 16, device="meta")
+        pt = torch.empty(3, 3, dtype=torch.int32, device="meta")
+        sl = torch.full((3,), 9, dtype=torch.int32, device="meta")
+        out = torch.ops.flashattn_tile.paged_decode_multi(q, k, k, pt, sl, 16, 0.25, 0)
+        sc = torch.empty(12, 2, device="meta")
+        outq = torch.ops.flashattn_tile.paged_decode_multi(q, k.to(torch.int8), k.to(torch.int8), pt, sl, 16, 0.25,
+                                                            2, sc, sc)
+    assert out.shape == (3, 4, 8, 16) and out.device.type == "meta" and outq.shape == (3, 4, 8, 16)
+    assert str(torch.ops.flashattn_tile.paged_decode_multi.default._schema) == (
+        "flashattn_tile::paged_decode_multi(Tensor q, Tensor k_cache, Tensor v_cache, Tensor page_table, "
+        "Tensor seq_lens, SymInt page_size, float softmax_scale, SymInt split_k, Tensor? k_scale=None, "
+        "Tensor? v_scale=None) -> Tensor")
+
+
 def test_compile_fullgraph_has_zero_graph_breaks():
     """Traced on meta tensors so no kernel runs on this CPU-only host; the GPU
     suite compiles and runs the same function on the device."""
@@ -90,8 +107,12 @@ def test_compile_fullgraph_has_zero_graph_breaks():
     def pre_paged(x):
         return torch.ops.flashattn_tile.prefill_paged(x, k, k, pt, sl, cu, 6, 16, True, 0.35) - 1
 
+    def dec_multi(x):
+        return torch.ops.flashattn_tile.paged_decode_multi(x, k, k, pt, sl, 16, 0.35, 0) * 3
+
     pre_arg = torch.empty(9, 4, 8, device="meta", dtype=torch.float16)
-    for fn, arg in ((dec, q), (pre, pre_arg), (pre_paged, pre_arg)):
+    multi_arg = torch.empty(2, 3, 4, 8, device="meta", dtype=torch.float16)
+    for fn, arg in ((dec, q), (pre, pre_arg), (pre_paged, pre_arg), (dec_multi, multi_arg)):
         explanation = torch._dynamo.explain(fn)(arg)
         assert explanation.graph_break_count == 0, explanation.break_reasons
         assert explanation.graph_count == 1
@@ -154,6 +175,11 @@ def test_backend_validation_and_routing_errors():
     # Decode routing reaches the kernel wrapper, which refuses CPU tensors.
     with pytest.raises(RuntimeError, match="ROCm device"):
         backend.forward(torch.randn(2, 1, 4, 8), cache, AttentionMetadata(softmax_scale=0.35))
+    # A [batch, q_len > 1, heads, dim] decode query routes to multi-token decode.
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        backend.forward(torch.randn(2, 3, 4, 8), cache, AttentionMetadata(softmax_scale=0.35))
+    with pytest.raises(ValueError, match="heads"):
+        backend.forward(torch.randn(2, 3, 5, 8), cache, AttentionMetadata())
 
 
 def test_native_availability_is_graceful():
