@@ -111,7 +111,11 @@ struct PagedRows {
 // a lane adds only its constant offset -- no per-load vector address math.
 // Rows at or past kv_len (last tile only) read slots of the last page and
 // are zeroed before they reach LDS (mask_tail).
-template <int LOADS, int RPL>
+// OFF32 (PG 3): the pool of this KV head lies within 2^31 bytes of its
+// first row, so it is one buffer and a load passes its row's byte offset as
+// the 32-bit scalar offset (page * page stride + slot * slot stride): one
+// multiply-add per load instead of a 64-bit address and a descriptor.
+template <int LOADS, int RPL, bool OFF32 = false>
 struct PagedRowsU {
   const uint8_t* base;
   const int32_t* pt_row;
@@ -120,6 +124,12 @@ struct PagedRowsU {
   uint32_t lane_off;  // row0 * st2 + col
   int pg[LOADS];      // page ids of the next tile (scalar registers)
   int cur;            // tile whose chunks are in the registers
+  __amdgpu_buffer_rsrc_t pool;  // OFF32: the KV head's pool from its first row
+
+  __device__ __forceinline__ void init_pool(int num_pages) {
+    (void)num_pages;  // the host checked every row offset against 2^31
+    if constexpr (OFF32) pool = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, kBufFlags);
+  }
 
   __device__ __forceinline__ int idx(int tile, int u) const {
     return min((tile * kBN + u * RPL) >> pshift, last_idx);
@@ -139,10 +149,15 @@ struct PagedRowsU {
     for (int u = 0; u < LOADS; ++u) {
       const int page = min(max(pg[u], 0), page_last);
       const int slot0 = (tile * kBN + u * RPL) & pmask;
-      const uint8_t* row_base = base + (int64_t)page * sp2 + (int64_t)slot0 * st2;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)row_base, (short)0, 0x7fffffff, kBufFlags);
-      dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, 0, 0));
+      if constexpr (OFF32) {
+        const uint32_t so = (uint32_t)page * (uint32_t)sp2 + (uint32_t)slot0 * (uint32_t)st2;
+        dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pool, (int)lane_off, (int)so, 0));
+      } else {
+        const uint8_t* row_base = base + (int64_t)page * sp2 + (int64_t)slot0 * st2;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)row_base, (short)0, 0x7fffffff, kBufFlags);
+        dst[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)lane_off, 0, 0));
+      }
     }
     cur = tile;
     fetch_ids(tile + 1);
@@ -341,7 +356,7 @@ void prefill_kernel(const PrefillParams p) {
   u32x4 kreg[LOADS], vreg[LOADS];
   // Paged streams: the same lane -> (row, chunk) mapping.  PG 1: page id per
   // lane and load; PG 2: page id per load (wave-uniform).
-  using Rows = std::conditional_t<PG == 2, PagedRowsU<LOADS, kRowsPerLoad>, PagedRows<LOADS, kRowsPerLoad>>;
+  using Rows = std::conditional_t<PG >= 2, PagedRowsU<LOADS, kRowsPerLoad, PG == 3>, PagedRows<LOADS, kRowsPerLoad>>;
   Rows kpr, vpr;
   if constexpr (PAGED) {
     const int32_t* pt_row = p.pt + (int64_t)b * p.pt_sb;
@@ -356,12 +371,14 @@ void prefill_kernel(const PrefillParams p) {
     kpr.pmask = vpr.pmask = (1 << p.pshift) - 1;
     kpr.page_last = vpr.page_last = p.num_pages - 1;
     kpr.row0 = vpr.row0 = tid / CPR;
-    if constexpr (PG == 2) {
+    if constexpr (PG >= 2) {
       kpr.kv_len = vpr.kv_len = kv_len;
       kpr.last_idx = vpr.last_idx = max(kv_len - 1, 0) >> p.pshift;
       kpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.k_st + 16 * (tid % CPR));
       vpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.v_st + 16 * (tid % CPR));
       kpr.cur = vpr.cur = 0;
+      kpr.init_pool(p.num_pages);
+      vpr.init_pool(p.num_pages);
     } else {
       kpr.kv_last = vpr.kv_last = max(kv_len - 1, 0);
       kpr.col = vpr.col = 16 * (tid % CPR);
@@ -394,7 +411,7 @@ void prefill_kernel(const PrefillParams p) {
     }
   };
   auto lstore_k = [&](int buf) {
-    if constexpr (PG == 2) kpr.mask_tail(kreg);
+    if constexpr (PG >= 2) kpr.mask_tail(kreg);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       const int cid = tid + 256 * u;
@@ -408,14 +425,14 @@ void prefill_kernel(const PrefillParams p) {
   int v_s = 0;
   auto convert_v = [&]() {
     if constexpr (VH) {
-      if constexpr (PG == 2) vpr.mask_tail(vreg);
+      if constexpr (PG >= 2) vpr.mask_tail(vreg);
       v_s = bf16_to_f16_scaled<LOADS>(vreg);
     }
   };
   auto lstore_v = [&](int buf) {
     if constexpr (VH) {
       if (lane == 0) vsc[buf][w] = v_s;
-    } else if constexpr (PG == 2) {
+    } else if constexpr (PG >= 2) {
       vpr.mask_tail(vreg);
     }
 #pragma unroll
@@ -741,7 +758,7 @@ void prefill_pp_kernel(const PrefillParams p) {
   u32x4 stage[LOADS];
   // PAGED only: this group's K or V stream (PG 1 per-lane page ids, PG 2
   // wave-uniform ones).
-  std::conditional_t<PG == 2, PagedRowsU<LOADS, kRowsPerLoad>, PagedRows<LOADS, kRowsPerLoad>> pr;
+  std::conditional_t<PG >= 2, PagedRowsU<LOADS, kRowsPerLoad, PG == 3>, PagedRows<LOADS, kRowsPerLoad>> pr;
   if constexpr (PAGED) {
     pr.base = (grp ? p.v : p.k) + 2 * (int64_t)kvh * sh;
     pr.pt_row = p.pt + (int64_t)b * p.pt_sb;
@@ -751,11 +768,12 @@ void prefill_pp_kernel(const PrefillParams p) {
     pr.pmask = (1 << p.pshift) - 1;
     pr.page_last = p.num_pages - 1;
     pr.row0 = gt / CPR;
-    if constexpr (PG == 2) {
+    if constexpr (PG >= 2) {
       pr.kv_len = kv_len;
       pr.last_idx = max(kv_len - 1, 0) >> p.pshift;
       pr.lane_off = (uint32_t)((gt / CPR) * st2 + 16 * (gt % CPR));
       pr.cur = 0;
+      pr.init_pool(p.num_pages);
     } else {
       pr.kv_last = max(kv_len - 1, 0);
       pr.col = 16 * (gt % CPR);
@@ -774,7 +792,7 @@ void prefill_pp_kernel(const PrefillParams p) {
     }
   };
   auto lstore = [&](int buf) {
-    if constexpr (PG == 2) pr.mask_tail(stage);
+    if constexpr (PG >= 2) pr.mask_tail(stage);
     if constexpr (VH) {
       if (grp == 1) {
         const int sw = bf16_to_f16_scaled<LOADS>(stage);
@@ -1242,12 +1260,24 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   prm.max_pages = a->max_pages;
   // One load covers 256 / (D / 8) rows (16 at D128, 32 at D64): with pages at
   // least that long its rows share a page and the page id is wave-uniform.
-  // FAT_PREFILL_PAGED_ROWS=lane forces the per-lane variant (tests).
   bool uniform = P >= 256 / (D / 8);
+  // Byte offset past the last row of the pool, from a KV head's first row:
+  // below 2^31 the uniform loads address the pool as one buffer (PG 3).
+  const int64_t kspan =
+      (int64_t)(a->num_pages - 1) * 2 * a->k_stride_page + (int64_t)(P - 1) * 2 * a->k_stride_slot + 2 * D;
+  const int64_t vspan =
+      (int64_t)(a->num_pages - 1) * 2 * a->v_stride_page + (int64_t)(P - 1) * 2 * a->v_stride_slot + 2 * D;
+  bool off32 = kspan < 0x7fffffffLL && vspan < 0x7fffffffLL;
+  // FAT_PREFILL_PAGED_ROWS=lane forces the per-lane variant, =wide the
+  // uniform one with 64-bit row addresses (tests).
   if (const char* force = getenv("FAT_PREFILL_PAGED_ROWS")) {
     if (!strcmp(force, "lane")) uniform = false;
+    else if (!strcmp(force, "wide")) off32 = false;
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  if (uniform && off32)
+    return launch_prefill<3>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
+                             "fat_prefill_paged", stream);
   if (uniform)
     return launch_prefill<2>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
                              "fat_prefill_paged", stream);

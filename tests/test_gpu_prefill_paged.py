@@ -129,17 +129,21 @@ def test_paged_prefill_validation():
         paged_prefill_attention(q, cache, cu[:2], 25, causal=False)
 
 
-@pytest.mark.parametrize("P", [32, 64])
+@pytest.mark.parametrize("P", [16, 32, 64])
 def test_paged_prefill_row_modes_agree(P, monkeypatch):
-    """Pages of >= 16 rows take the wave-uniform addressing; forcing the
+    """Pages of >= 16 rows take the wave-uniform addressing (32-bit pool
+    offsets for a pool under 2 GiB); forcing 64-bit row addresses or the
     per-lane addressing on the same inputs must give identical bits."""
+    print(f"paged P{P} row modes", flush=True)
     lens_k, lens_q = [900, 70, 129], [300, 70, 1]
     q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, P, torch.bfloat16, seed=P + 1)
     uni = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    monkeypatch.setenv("FAT_PREFILL_PAGED_ROWS", "wide")
+    wide = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
     monkeypatch.setenv("FAT_PREFILL_PAGED_ROWS", "lane")
     lane = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
     torch.cuda.synchronize()
-    assert torch.equal(uni, lane)
+    assert torch.equal(uni, lane) and torch.equal(uni, wide)
     assert_parity(uni, _ref32(q, cache, cu, True), label=f"paged P{P} uniform rows")
 
 
