@@ -310,7 +310,8 @@ def bench_prefill(args, device, seq=8192):
             "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"],
                          "traffic": (_traffic_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128")
-                                     if name == "f16" else None)},
+                                     if name == "f16" else None),
+                         "mfma_busy": _mfma_busy_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128", name)},
         }
     res["workload"] = f"prefill_causal_seq{seq}_h32_kv8_d128"
     res["steps"] = steps
@@ -679,15 +680,24 @@ def all_configs(args, device):
     return rows
 
 
-def _traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs (profiles/traffic.json)."""
+def _profile_entry(workload: str) -> dict:
+    """The rocprofv3 PMC measurements of a workload (profiles/traffic.json)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as fh:
-            data = json.load(fh)
-        return data.get(workload, {}).get("bytes_per_launch")
+            return json.load(fh).get(workload, {})
     except (OSError, ValueError):
-        return None
+        return {}
+
+
+def _traffic_from_profiles(workload: str):
+    """HBM bytes per launch measured by rocprofv3 PMC runs."""
+    return _profile_entry(workload).get("bytes_per_launch")
+
+
+def _mfma_busy_from_profiles(workload: str, dtype: str):
+    """Fraction of the kernel's cycles the MFMA pipe was busy (PMC run)."""
+    return _profile_entry(workload).get("mfma_busy", {}).get(dtype)
 
 
 def main():
