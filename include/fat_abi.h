@@ -84,6 +84,9 @@ enum fat_status {
  *   v_scale  same as k_scale
  *   page_table int32 [batch, max_pages]  (row stride page_table_stride)
  *   seq_lens int32 [batch], every entry in [1, max_pages*page_size]
+ * page_size is a power of two of at least the rows one 16-byte load per lane
+ * covers: 4 (fp16/bf16, head_dim 128), 8 (fp16/bf16 64; int8/fp8 128) or 16
+ * (int8/fp8 64); smaller pages return FAT_E_UNSUPPORTED.
  *   out      [batch, num_heads, head_dim]          q_dtype
  * Strides are in elements; the head_dim axis must be contiguous.
  *
