@@ -534,6 +534,55 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
                     "sample": f"1 of {len(lens)} sequences, min of {reps}"}}
 
 
+def _graph_decode_row(name, B, ctx, device, args, hq=32, hkv=8, d=128, page=16, layers=32):
+    """Per-launch cost of a small decode in a step of `layers` launches (one
+    per model layer; all on the same cache here): launched eagerly from Python
+    (paged_decode_launch: ctypes argument block + launch) and replayed from
+    one HIP graph that captured the whole step."""
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd import PagedKVCache, _hip
+    from flashattntile_amd.kernels.decode import paged_decode_launch
+
+    q, pools, table, seq, _, _ = _paged_inputs([ctx] * B, hq, hkv, d, page, torch.float16, seed=17, device=device,
+                                               copies=1)
+    k, v, _, _ = pools[0]
+    cache = PagedKVCache(k, v, table, seq, page)
+    sk, pps, waves, kern, _ = _product_launch(q, pools, table, seq, page, ctx, B * table.shape[1])
+    kname = {0: None, 1: "valu", 2: "mfma"}[kern]
+    out = torch.empty_like(q)
+    ws = torch.empty(max(1, _hip.decode_workspace_bytes(B, hq, d, sk)), dtype=torch.uint8, device=device)
+
+    def launch():
+        paged_decode_launch(q, cache, d ** -0.5, sk, out=out, workspace=ws, waves_per_group=waves,
+                            pages_per_split=pps, kernel=kname)
+
+    def step():
+        for _ in range(layers):
+            launch()
+
+    stream = torch.cuda.current_stream(device)
+    steps = max(10, args.steps // 20)
+    eager = _time_steps(lambda i: step(), steps, 3, stream) / layers
+    side = torch.cuda.Stream(device)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        step()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    replay = _time_steps(lambda i: graph.replay(), steps, 3, stream) / layers
+    nbytes = 4096 * B * ctx + 16384 * B
+    del pools, cache
+    torch.cuda.empty_cache()
+    return {"config": name, "kind": "decode_graph", "value": round(replay * 1e3, 2), "unit": "us/call",
+            "frac": round(nbytes / (replay * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "us": round(replay * 1e3, 2),
+            "eager_us": round(eager * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "cpu": None}
+
+
 def _quantize_row(name, src_dtype, mode, device, args, pages=8192, page=16, hkv=8, d=128):
     """fat_quantize_pages over a whole K pool (the headline cache's 8192 pages);
     two pools alternate.  Bytes = read src + write codes + write scales."""
@@ -630,8 +679,10 @@ def all_configs(args, device):
         if row is None:
             return
         rows.append(row)
+        tail = (f"cpu {row['cpu']['value']} {row['cpu']['unit']}" if row.get("cpu")
+                else f"eager Python launch {row.get('eager_us')} us/call")
         print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
-              f"{row['us']:9.1f} us)  cpu {row['cpu']['value']} {row['cpu']['unit']}", file=sys.stderr, flush=True)
+              f"{row['us']:9.1f} us)  {tail}", file=sys.stderr, flush=True)
 
     # fp16 decode sweep (and bf16 at the headline shape)
     for B in (1, 8, 32, 128):
@@ -665,6 +716,9 @@ def all_configs(args, device):
     # Multi-token (speculative) decode: T query tokens per sequence
     for T in (2, 4, 8):
         emit(_multi_decode_row(f"decode fp16 multi-token T{T} B32 ctx4096", [4096] * 32, T, device, args))
+    # small decodes: Python-launched vs replayed from a HIP graph
+    for B, ctx in ((1, 1024), (8, 1024), (32, 128)):
+        emit(_graph_decode_row(f"decode fp16 B{B} ctx{ctx} graph replay (32/step)", B, ctx, device, args))
     # Paged (chunked) prefill: K/V through the page table (page 16)
     for dt, dn in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         emit(_paged_prefill_row(f"prefill paged {dn} causal L8192 P16", [8192], [8192], dt, device, args))
