@@ -561,9 +561,21 @@ def _graph_decode_row(name, B, ctx, device, args, hq=32, hkv=8, d=128, page=16, 
         for _ in range(layers):
             launch()
 
+    from flashattntile_amd.kernels.decode import DecodeLaunch
+
+    plan = DecodeLaunch(q, cache, d ** -0.5, config={"split_k": sk, "pages_per_split": pps,
+                                                     "num_warps": waves or None, "kernel": kname},
+                        max_len=ctx, total_pages=B * table.shape[1])
+    handle = int(torch.cuda.current_stream(device).cuda_stream)
+
+    def plan_step():
+        for _ in range(layers):
+            plan.run(q, out, stream=handle)
+
     stream = torch.cuda.current_stream(device)
     steps = max(10, args.steps // 20)
     eager = _time_steps(lambda i: step(), steps, 3, stream) / layers
+    planned = _time_steps(lambda i: plan_step(), steps, 3, stream) / layers
     side = torch.cuda.Stream(device)
     side.wait_stream(stream)
     with torch.cuda.stream(side):
@@ -579,7 +591,7 @@ def _graph_decode_row(name, B, ctx, device, args, hq=32, hkv=8, d=128, page=16, 
     torch.cuda.empty_cache()
     return {"config": name, "kind": "decode_graph", "value": round(replay * 1e3, 2), "unit": "us/call",
             "frac": round(nbytes / (replay * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "us": round(replay * 1e3, 2),
-            "eager_us": round(eager * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "eager_us": round(eager * 1e3, 2), "plan_us": round(planned * 1e3, 2), "bytes": nbytes, "split_k": sk,
             "cpu": None}
 
 
@@ -680,7 +692,7 @@ def all_configs(args, device):
             return
         rows.append(row)
         tail = (f"cpu {row['cpu']['value']} {row['cpu']['unit']}" if row.get("cpu")
-                else f"eager Python launch {row.get('eager_us')} us/call")
+                else f"eager Python launch {row.get('eager_us')} us/call, DecodeLaunch.run {row.get('plan_us')} us/call")
         print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
               f"{row['us']:9.1f} us)  {tail}", file=sys.stderr, flush=True)
 

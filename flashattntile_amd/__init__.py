@@ -16,7 +16,8 @@ from __future__ import annotations
 __version__ = "0.1.0"
 
 from . import ops as _ops  # noqa: F401  (registers the custom ops)
-from .kernels.decode import paged_decode_attention, paged_decode_attention_fp8, paged_decode_attention_multi
+from .kernels.decode import (DecodeLaunch, paged_decode_attention, paged_decode_attention_fp8,
+                             paged_decode_attention_multi)
 from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .ops import (PAGED_DECODE_MULTI_OP, PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, PREFILL_PAGED_OP,
                   paged_decode, paged_decode_multi, paged_decode_quant, prefill_paged, prefill_varlen)
@@ -39,6 +40,7 @@ __all__ = [
     "paged_decode_attention",
     "paged_decode_attention_fp8",
     "paged_decode_attention_multi",
+    "DecodeLaunch",
     "prefill_attention",
     "PagedKVCache",
     "allocate",

@@ -364,6 +364,31 @@ def paged_decode(
 
     ``q``/``out`` are ``[B, H, D]`` (one query per sequence) or
     ``[B, T, H, D]`` (multi-token decode, ``q_len = T``)."""
+    a = decode_args(q, k_cache, v_cache, page_table, seq_lens, out, page_size, softmax_scale, split_k,
+                    workspace=workspace, k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group,
+                    pages_per_split=pages_per_split, kernel=kernel)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
+
+
+def decode_args(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    out: torch.Tensor,
+    page_size: int,
+    softmax_scale: float,
+    split_k: int,
+    workspace: torch.Tensor | None = None,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    waves_per_group: int = 0,
+    pages_per_split: int = 0,
+    kernel: int = KERNEL_AUTO,
+) -> DecodeArgs:
+    """The ``fat_decode_args`` block of a decode launch (see paged_decode)."""
     multi = q.dim() == 4
     a = DecodeArgs()
     a.q = _ptr(q)
@@ -401,8 +426,12 @@ def paged_decode(
     a.pages_per_split = int(pages_per_split)
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
-    handle = current_stream_handle(q.device) if stream is None else stream
-    _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
+    return a
+
+
+def decode_with_args(a: DecodeArgs, stream: int) -> None:
+    """Enqueue ``fat_paged_decode`` with a prepared argument block."""
+    _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(stream)), "fat_paged_decode")
 
 
 def prefill_varlen(

@@ -45,6 +45,7 @@ __all__ = [
     "paged_decode_attention_multi",
     "paged_decode_launch",
     "resolve_decode_config",
+    "DecodeLaunch",
 ]
 
 # split_k None -> MI355X partition heuristic (split_k and pages_per_split from
@@ -331,3 +332,80 @@ def paged_decode_attention_multi(
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], scales=sc,
                                waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"],
                                kernel=cfg["kernel"])
+
+
+class DecodeLaunch:
+    """A decode launch prepared once and run every step (plan / run).
+
+    Construction validates ``q`` and ``cache`` (one synchronisation, as
+    :func:`paged_decode_attention` does, unless ``max_len`` and
+    ``total_pages`` are given), resolves the launch (``config``, else the
+    tuned store, else the heuristic), allocates the split-K workspace and
+    fills the ``fat_decode_args`` block.  :meth:`run` then only writes the
+    query and output addresses into that block and enqueues
+    ``fat_paged_decode``: no validation, synchronisation or allocation, about
+    the cost of one ctypes call.  The page table and seq_lens are read on the
+    device at every run, so the serving engine updates them in place.  ``q``
+    and ``out`` passed to :meth:`run` must have the dtype, shape and strides
+    of the ``q`` given here (``out``: contiguous).  ``q`` is ``[B, H, D]`` or
+    ``[B, T, H, D]`` (multi-token decode); ``scales`` selects an int8 /
+    float8_e4m3fn cache.
+    """
+
+    def __init__(self, q: torch.Tensor, cache: PagedKVCache, softmax_scale: float | None = None,
+                 config: dict | None = None, scales=None, max_len: int | None = None,
+                 total_pages: int | None = None) -> None:
+        multi = q.dim() == 4
+        if max_len is None or total_pages is None:
+            max_len, total_pages = _validate_decode_inputs(q, cache, multi=multi)
+        q_len = int(q.shape[1]) if multi else 1
+        cfg = _resolve_config(config, q, cache, max_len, total_pages, q_len=q_len)
+        _require_rocm(q, cache, "DecodeLaunch")
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"DecodeLaunch: dtype {q.dtype} is not fp16/bf16")
+        quantized = cache.k_cache.dtype in _QUANT_DTYPES
+        if quantized != (scales is not None):
+            raise ValueError("an int8/float8 cache needs scales, and only such a cache takes them")
+        if not quantized and cache.k_cache.dtype != q.dtype:
+            raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
+        if not q.is_contiguous():
+            raise ValueError("DecodeLaunch: q must be contiguous")
+        k_scale = v_scale = None
+        if quantized:
+            k_scale = (scales["k"] if isinstance(scales, dict) else scales.k).contiguous()
+            v_scale = (scales["v"] if isinstance(scales, dict) else scales.v).contiguous()
+            expected = (cache.num_pages, cache.num_kv_heads)
+            if tuple(k_scale.shape) != expected or tuple(v_scale.shape) != expected:
+                raise ValueError(f"scales must have shape {expected}, got {tuple(k_scale.shape)}")
+            if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
+                raise ValueError("scales must be float32")
+        if cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
+            raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
+        self.config = cfg
+        self.softmax_scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
+        rows = q.shape[0] * q_len
+        need = _hip.decode_workspace_bytes(rows, q.shape[-2], q.shape[-1], cfg["split_k"])
+        self.workspace = torch.empty(max(1, need), dtype=torch.uint8, device=q.device) if need else None
+        self._keep = (cache, k_scale, v_scale)  # the argument block points into these
+        self._shape, self._dtype = tuple(q.shape), q.dtype
+        self._device = q.device
+        self._args = _hip.decode_args(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, q,
+                                      cache.page_size, self.softmax_scale, cfg["split_k"],
+                                      workspace=self.workspace, k_scale=k_scale, v_scale=v_scale,
+                                      waves_per_group=cfg["num_warps"] or 0,
+                                      pages_per_split=cfg["pages_per_split"], kernel=_KERNEL_CODES[cfg["kernel"]])
+
+    def run(self, q: torch.Tensor, out: torch.Tensor | None = None, stream: int | None = None) -> torch.Tensor:
+        """Decode ``q`` into ``out`` (default: a new tensor) on ``stream``
+        (a hipStream_t handle; default torch's current stream)."""
+        if tuple(q.shape) != self._shape or q.dtype != self._dtype or not q.is_contiguous():
+            raise ValueError(f"DecodeLaunch.run: q must be a contiguous {self._dtype} tensor of shape {self._shape}")
+        if out is None:
+            out = torch.empty_like(q)
+        elif tuple(out.shape) != self._shape or out.dtype != self._dtype or not out.is_contiguous():
+            raise ValueError(f"DecodeLaunch.run: out must be a contiguous {self._dtype} tensor of shape {self._shape}")
+        a = self._args
+        a.q = q.data_ptr()
+        a.out = out.data_ptr()
+        _hip.decode_with_args(a, _hip.current_stream_handle(self._device) if stream is None else stream)
+        return out

@@ -152,3 +152,41 @@ def test_serving_step_graph_append_then_decode(mode):
             for a, b in zip(parts(mirror), parts(twin_mirror)):
                 assert torch.equal(a, b), f"{label}: quantised copy after replay {i}"
         assert torch.equal(out, ref), f"{label}: output after replay {i}"
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16-mqa", "int8", "multi"])
+def test_decode_launch_plan_runs_match_wrappers(kind):
+    """DecodeLaunch (plan once, run per step) gives the wrappers' bits, also
+    after seq_lens and the pages change in place between runs."""
+    from flashattntile_amd import DecodeLaunch, paged_decode_attention, paged_decode_attention_multi
+    from flashattntile_amd import paged_decode_attention_fp8
+
+    print(f"decode plan {kind}", flush=True)
+    dtype = torch.bfloat16 if kind == "bf16-mqa" else torch.float16
+    hk = 1 if kind == "bf16-mqa" else 8
+    lens = [40, 700, 129, 2000]
+    k, v, pt, sl = make_paged([n + 8 for n in lens], hk, 128, 16, dtype, seed=21, device=DEV, poison=False)
+    sl.copy_(torch.tensor(lens, dtype=torch.int32))
+    cache = PagedKVCache(k, v, pt, sl, 16)
+    scales = None
+    if kind == "int8":
+        cache, scales = quantize_cache(cache, "int8")
+    g = torch.Generator(device=DEV).manual_seed(22)
+    shape = (len(lens), 3, 32, 128) if kind == "multi" else (len(lens), 32, 128)
+    q = torch.randn(shape, generator=g, device=DEV).to(dtype)
+    plan = DecodeLaunch(q, cache, softmax_scale=0.09, scales=scales, config={"split_k": 3})
+    out = torch.empty_like(q)
+    for i in range(3):
+        q.copy_(torch.randn(shape, generator=g, device=DEV).to(dtype))
+        cache.seq_lens.add_(2)  # the engine appends in place; the plan reads lengths on the device
+        plan.run(q, out)
+        if kind == "multi":
+            ref = paged_decode_attention_multi(q, cache, softmax_scale=0.09, config={"split_k": 3})
+        elif kind == "int8":
+            ref = paged_decode_attention_fp8(q, cache, scales, softmax_scale=0.09, config={"split_k": 3})
+        else:
+            ref = paged_decode_attention(q, cache, softmax_scale=0.09, config={"split_k": 3})
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"decode plan {kind} run {i}"
+    with pytest.raises(ValueError, match="shape"):
+        plan.run(q[:2].contiguous())

@@ -137,6 +137,8 @@ def test_cpu_tensors_raise_instead_of_falling_back():
     cache2 = _cache(batch=2, length=6, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="ROCm device"):
         fat.paged_prefill_attention(qp, cache2, cu, 6)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fat.DecodeLaunch(q, cache)
 
 
 def test_backend_kv_cache_shape_matches_allocate():
