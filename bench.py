@@ -658,6 +658,17 @@ def _append_row(name, mode, device, args, B=32, ctx=4000, page=16, hkv=8, d=128)
 
     steps = max(64, args.steps // 2)
     ms = _time_steps(step, steps, 8, stream)
+    from flashattntile_amd.paging import AppendLaunch
+
+    plan = AppendLaunch(cache, quantized=mirror)
+    handle = int(stream.cuda_stream)
+
+    def plan_step(i):
+        if i % 64 == 0:
+            lens.fill_(ctx)
+        plan.run(nk, nv, stream=handle)
+
+    plan_ms = _time_steps(plan_step, steps, 8, stream)
     nbytes = 2 * B * hkv * d * 2
     if mode:
         nbytes += 2 * B * hkv * (page * d * (2 + 1) + 4)
@@ -679,6 +690,7 @@ def _append_row(name, mode, device, args, B=32, ctx=4000, page=16, hkv=8, d=128)
     us = ms * 1e3
     return {"config": name, "kind": "kv_write", "value": round(us, 2), "unit": "us/call",
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "us": round(us, 2), "bytes": nbytes,
+            "plan_us": round(plan_ms * 1e3, 2),
             "cpu": {"value": round(best * 1e6, 1), "unit": "us/call (torch path, 4 sequences)",
                     "sample": f"4 of {B} sequences, min of {reps}"}}
 
@@ -691,7 +703,8 @@ def all_configs(args, device):
         if row is None:
             return
         rows.append(row)
-        tail = (f"cpu {row['cpu']['value']} {row['cpu']['unit']}" if row.get("cpu")
+        tail = (f"cpu {row['cpu']['value']} {row['cpu']['unit']}"
+                + (f"; AppendLaunch.run {row['plan_us']} us/call" if "plan_us" in row else "") if row.get("cpu")
                 else f"eager Python launch {row.get('eager_us')} us/call, DecodeLaunch.run {row.get('plan_us')} us/call")
         print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
               f"{row['us']:9.1f} us)  {tail}", file=sys.stderr, flush=True)

@@ -21,7 +21,8 @@ from .kernels.decode import (DecodeLaunch, paged_decode_attention, paged_decode_
 from .kernels.prefill import paged_prefill_attention, prefill_attention
 from .ops import (PAGED_DECODE_MULTI_OP, PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, PREFILL_PAGED_OP,
                   paged_decode, paged_decode_multi, paged_decode_quant, prefill_paged, prefill_varlen)
-from .paging import PagedKVCache, allocate, append_tokens, gather_contiguous, gather_paged, validate_cache
+from .paging import (AppendLaunch, PagedKVCache, allocate, append_tokens, gather_contiguous, gather_paged,
+                     validate_cache)
 from .quant import QuantScales, dequantize_cache, kv_bytes_per_token, quantize_cache
 
 __all__ = [
@@ -45,6 +46,7 @@ __all__ = [
     "PagedKVCache",
     "allocate",
     "append_tokens",
+    "AppendLaunch",
     "gather_contiguous",
     "gather_paged",
     "validate_cache",

@@ -557,6 +557,27 @@ def append_kv(
     stream: int | None = None,
 ) -> None:
     """Enqueue ``fat_append_kv`` for already-validated device tensors."""
+    a = append_args(new_k, new_v, k_cache, v_cache, page_table, seq_lens, page_size, quant_k=quant_k,
+                    quant_v=quant_v, k_scale=k_scale, v_scale=v_scale, advance=advance)
+    handle = current_stream_handle(k_cache.device) if stream is None else stream
+    _check(lib().fat_append_kv(ctypes.byref(a), _c_vp(handle)), "fat_append_kv")
+
+
+def append_args(
+    new_k: torch.Tensor,
+    new_v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    page_size: int,
+    quant_k: torch.Tensor | None = None,
+    quant_v: torch.Tensor | None = None,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+    advance: bool = True,
+) -> AppendArgs:
+    """The ``fat_append_args`` block of an append (see append_kv)."""
     a = AppendArgs()
     a.new_k = _ptr(new_k)
     a.new_v = _ptr(new_v)
@@ -588,5 +609,9 @@ def append_kv(
     a.max_pages = page_table.shape[1]
     a.dtype = dtype_code(k_cache.dtype)
     a.advance = 1 if advance else 0
-    handle = current_stream_handle(k_cache.device) if stream is None else stream
-    _check(lib().fat_append_kv(ctypes.byref(a), _c_vp(handle)), "fat_append_kv")
+    return a
+
+
+def append_with_args(a: AppendArgs, stream: int) -> None:
+    """Enqueue ``fat_append_kv`` with a prepared argument block."""
+    _check(lib().fat_append_kv(ctypes.byref(a), _c_vp(stream)), "fat_append_kv")

@@ -32,6 +32,7 @@ __all__ = [
     "validate_cache",
     "allocate",
     "append_tokens",
+    "AppendLaunch",
     "gather_paged",
     "gather_contiguous",
 ]
@@ -300,6 +301,65 @@ def _append_hip(cache: PagedKVCache, new_k: torch.Tensor, new_v: torch.Tensor, m
         qk, qv, sk, sv = mirror
     _hip.append_kv(nk, nv, cache.k_cache, cache.v_cache, pt, cache.seq_lens, cache.page_size,
                    quant_k=qk, quant_v=qv, k_scale=sk, v_scale=sv, advance=True)
+
+
+class AppendLaunch:
+    """An append prepared once and run every decode step (plan / run).
+
+    Construction checks the cache (and its int8/fp8 copy ``quantized``, as
+    :func:`append_tokens` takes it) and fills the ``fat_append_args`` block;
+    :meth:`run` writes the two new-token addresses and enqueues
+    ``fat_append_kv`` on the stream: one ctypes call, no synchronisation, no
+    host bounds check (entries past the table or a bad page id are skipped
+    by the kernel and their lengths left, as ``append_tokens(...,
+    validate=False)`` does).  ``new_k`` / ``new_v`` passed to :meth:`run` must
+    be contiguous ``[batch, num_kv_heads, head_dim]`` in the cache dtype.
+    ROCm tensors only.
+    """
+
+    def __init__(self, cache: PagedKVCache, quantized=None) -> None:
+        from . import _hip
+
+        _check_layout(cache)
+        if not cache.k_cache.is_cuda:
+            raise RuntimeError("AppendLaunch: the cache must live on a ROCm device (the HIP kernels run there)")
+        dev = cache.k_cache.device
+        _require(cache.page_table.device == dev and cache.seq_lens.device == dev,
+                 "page_table and seq_lens must live on the cache device")
+        _require(cache.k_cache.stride(3) == 1 and cache.v_cache.stride(3) == 1, "the head_dim axis must be contiguous")
+        _require(cache.seq_lens.is_contiguous(), "seq_lens must be contiguous (it is advanced in place)")
+        _require(cache.page_table.stride(1) == 1, "page_table rows must be contiguous")
+        mirror = _quant_pair(cache, quantized) if quantized is not None else None
+        qk = qv = sk = sv = None
+        if mirror is not None:
+            qk, qv, sk, sv = mirror
+            _require(qk.stride(3) == 1 and qv.stride(3) == 1,
+                     "the head_dim axis of the quantised pages must be contiguous")
+            _require(sk.stride() == sv.stride(), "k and v scales must share strides")
+        self._shape = (cache.batch_size, cache.num_kv_heads, cache.head_dim)
+        self._dtype = cache.k_cache.dtype
+        self._device = dev
+        self._keep = (cache, mirror)
+        tmpl = torch.empty(self._shape, dtype=self._dtype, device="meta")
+        self._args = _hip.append_args(tmpl, tmpl, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens,
+                                      cache.page_size, quant_k=qk, quant_v=qv, k_scale=sk, v_scale=sv, advance=True)
+
+    def run(self, new_k: torch.Tensor, new_v: torch.Tensor, stream: int | None = None) -> None:
+        """Append ``new_k`` / ``new_v`` at ``seq_lens`` and advance it, on
+        ``stream`` (a hipStream_t handle; default torch's current stream)."""
+        from . import _hip
+
+        for t in (new_k, new_v):
+            if tuple(t.shape) != self._shape or t.dtype != self._dtype or not t.is_contiguous() \
+                    or t.device != self._device:
+                raise ValueError(f"AppendLaunch.run: new_k / new_v must be contiguous {self._dtype} "
+                                 f"{self._shape} tensors on {self._device}")
+        if self._shape[0] == 0:
+            return
+        a = self._args
+        a.new_k = new_k.data_ptr()
+        a.new_v = new_v.data_ptr()
+        _hip.append_with_args(a, _hip.current_stream_handle(self._device) if stream is None else stream)
 
 
 def gather_paged(

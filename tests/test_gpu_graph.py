@@ -190,3 +190,34 @@ def test_decode_launch_plan_runs_match_wrappers(kind):
         assert torch.equal(out, ref), f"decode plan {kind} run {i}"
     with pytest.raises(ValueError, match="shape"):
         plan.run(q[:2].contiguous())
+
+
+@pytest.mark.parametrize("mode", [None, "int8"])
+def test_append_launch_plan_matches_append_tokens(mode):
+    """AppendLaunch.run (plan once) writes the same pages, lengths and
+    quantised copy as append_tokens on a twin cache, step after step."""
+    from flashattntile_amd import AppendLaunch
+
+    print(f"append plan mode={mode}", flush=True)
+    lens = [3, 64, 17, 200]
+    k, v, pt, sl = make_paged([n + 8 for n in lens], 8, 128, 16, torch.bfloat16, seed=31, device=DEV,
+                              poison=False)
+    sl.copy_(torch.tensor(lens, dtype=torch.int32))
+    cache = PagedKVCache(k, v, pt, sl, 16)
+    twin = PagedKVCache(k.clone(), v.clone(), pt.clone(), sl.clone(), 16)
+    m1 = quantize_cache(cache, mode) if mode else None
+    m2 = quantize_cache(twin, mode) if mode else None
+    plan = AppendLaunch(cache, quantized=m1)
+    g = torch.Generator(device=DEV).manual_seed(32)
+    for i in range(5):
+        nk = torch.randn(len(lens), 8, 128, generator=g, device=DEV).bfloat16()
+        nv = torch.randn(len(lens), 8, 128, generator=g, device=DEV).bfloat16()
+        plan.run(nk, nv)
+        append_tokens(twin, nk, nv, quantized=m2, validate=False)
+        torch.cuda.synchronize()
+        assert torch.equal(cache.seq_lens, twin.seq_lens) and torch.equal(cache.k_cache, twin.k_cache) \
+            and torch.equal(cache.v_cache, twin.v_cache), f"append plan step {i}"
+        if mode:
+            assert torch.equal(m1[0].k_cache, m2[0].k_cache) and torch.equal(m1[1].v, m2[1].v), f"copy step {i}"
+    with pytest.raises(ValueError, match="contiguous"):
+        plan.run(nk.float(), nv)

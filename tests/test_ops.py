@@ -139,6 +139,8 @@ def test_cpu_tensors_raise_instead_of_falling_back():
         fat.paged_prefill_attention(qp, cache2, cu, 6)
     with pytest.raises(RuntimeError, match="ROCm device"):
         fat.DecodeLaunch(q, cache)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fat.AppendLaunch(cache)
 
 
 def test_backend_kv_cache_shape_matches_allocate():
