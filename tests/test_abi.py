@@ -185,8 +185,8 @@ def test_append_argument_errors_are_reported():
 
 
 def test_integration_stubs_match_the_abi():
-    """The ctypes stubs shown in INTEGRATION.md lay out their structs exactly
-    as the bindings (and so the header) do."""
+    """The ctypes stubs the integration guide shows a maintainer lay out
+    their structs exactly as the bindings (and so the header) do."""
     text = (ROOT / "INTEGRATION.md").read_text()
     found = 0
     for block in re.findall(r"```python\n(.*?)```", text, re.S):
