@@ -35,6 +35,7 @@ KERNEL_DECODE_VALU = 1
 KERNEL_DECODE_MFMA = 2
 KERNEL_PREFILL_PINGPONG = 1
 KERNEL_PREFILL_4WAVE = 2
+KERNEL_PREFILL_4WAVE_SPLIT = 3
 
 EXPORTED_SYMBOLS = (
     "fat_abi_version",

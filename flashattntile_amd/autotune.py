@@ -344,10 +344,11 @@ def build_config_space(kind: str, *, batch: int = 1, num_heads: int = 32, num_kv
     4/8-wave workgroups times the VALU and MFMA kernel families, plus the
     :func:`decode_partition` pick; the VALU kernel is left out for
     multi-token decode, which only the MFMA kernel serves.  ``prefill`` and
-    ``prefill_paged``: the 8-wave ping-pong and the 4-wave kernel.
+    ``prefill_paged``: the 8-wave ping-pong, the 4-wave kernel and its 8-wave
+    key-split form.
     """
     if kind in ("prefill", "prefill_paged"):
-        return [{"kernel": "pingpong"}, {"kernel": "4wave"}]
+        return [{"kernel": "pingpong"}, {"kernel": "4wave"}, {"kernel": "4wave_split"}]
     if kind != "decode":
         raise ValueError(f"unknown kind {kind!r}")
     max_pages = max(1, int(max_pages))

@@ -84,6 +84,7 @@ struct PagedRows {
   int64_t sp2;          // page stride, bytes
   int64_t st2;          // slot stride, bytes
   int pshift, pmask, kv_last, page_last, row0, col;
+  int tstep = 1;  // tile distance between this stream's consecutive loads
   int pg[LOADS];
 
   __device__ __forceinline__ int row_of(int tile, int u) const {
@@ -102,7 +103,7 @@ struct PagedRows {
       const int j = row_of(tile, u);
       dst[u] = *reinterpret_cast<const u32x4*>(base + (int64_t)pg[u] * sp2 + (int64_t)(j & pmask) * st2 + col);
     }
-    fetch_ids(tile + 1);
+    fetch_ids(tile + tstep);
   }
 };
 
@@ -124,6 +125,7 @@ struct PagedRowsU {
   uint32_t lane_off;  // row0 * st2 + col
   int pg[LOADS];      // page ids of the next tile (scalar registers)
   int cur;            // tile whose chunks are in the registers
+  int tstep = 1;      // tile distance between this stream's consecutive loads
   __amdgpu_buffer_rsrc_t pool;  // OFF32: the KV head's pool from its first row
 
   __device__ __forceinline__ void init_pool(int num_pages) {
@@ -160,7 +162,7 @@ struct PagedRowsU {
       }
     }
     cur = tile;
-    fetch_ids(tile + 1);
+    fetch_ids(tile + tstep);
   }
   __device__ __forceinline__ void mask_tail(u32x4 (&dst)[LOADS]) const {
     if (cur * kBN + kBN > kv_len) {  // wave-uniform
@@ -251,14 +253,30 @@ __device__ __forceinline__ void v_scale_offsets(const int* sc, int g, int& e_acc
 // exceeds it by more than this many log2 units; p = 2^(x - m) then stays
 // below 2^kLazy, which fp16/bf16 P and the fp32 sums hold exactly as well.
 constexpr float kLazy = 8.0f;
-#ifndef FAT_PF_PP_MIN
-#define FAT_PF_PP_MIN 512
+#ifndef FAT_PF_PP_MIN_FULL
+#define FAT_PF_PP_MIN_FULL 256
+#endif
+#ifndef FAT_PF_PP_MIN_CAUSAL
+#define FAT_PF_PP_MIN_CAUSAL 256
+#endif
+#ifndef FAT_PF_SPLIT_MAX
+#define FAT_PF_SPLIT_MAX 256
+#endif
+#ifndef FAT_PF_SPLIT_TILES
+#define FAT_PF_SPLIT_TILES 8
+#endif
+#ifndef FAT_PF_SPLIT_LONG
+#define FAT_PF_SPLIT_LONG 32
 #endif
 
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
-template <typename T, int D, bool CAUSAL, bool POS, int PG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// NG = 2: two groups of 4 waves take alternate K/V tiles for the same query
+// rows (group g tiles g, g + 2, ...) and merge (m, l, O) through LDS at the
+// end, halving the tile chain of a query block: for grids too small to
+// give every CU more than one workgroup.
+template <typename T, int D, bool CAUSAL, bool POS, int PG, int NG>
+__global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;        // MFMA k-steps of S^T over the head dim
   constexpr int DB = D / 32;        // 32-row blocks of O^T
@@ -270,14 +288,14 @@ void prefill_kernel(const PrefillParams p) {
 
   // Two K/V buffers: tile t+1 is written while tile t is read, so one
   // workgroup barrier per tile suffices.
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * K_RS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * V_RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[NG][2][kBN * K_RS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[NG][2][kBN * V_RS];
   // bf16: V is staged as fp16, each wave's rows scaled by 2^-s (s = 0 unless
   // some |v| >= 2^15; vsc[buffer][wave]), and PV runs as one fp16 MFMA; the
   // softmax folds 2^(s - e_acc) into P and O is kept as acc * 2^e_acc (see
   // prefill_pp_kernel).
   constexpr bool VH = std::is_same<T, BF16>::value;
-  __shared__ __attribute__((aligned(16))) int vsc[2][4];
+  __shared__ __attribute__((aligned(16))) int vsc[NG][2][4];
 
   // ---- work item: longest query blocks first; heads sharing a KV head
   // ---- land on the same XCD (consecutive ids go to consecutive XCDs).
@@ -299,7 +317,9 @@ void prefill_kernel(const PrefillParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = NG > 1 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;  // key-tile group
+  const int gt = tid & 255;                                               // thread in the group
+  const int w = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);           // wave in the group
   const int g = lane >> 5;   // k-group of the MFMA operands
   const int li = lane & 31;  // query column of this lane
   const int shift = kv_len - q_len;
@@ -322,7 +342,13 @@ void prefill_kernel(const PrefillParams p) {
 
   int hi = kv_len;
   if (CAUSAL) hi = min(kv_len, (mb + 1) * kBM + shift);
-  const int n_tiles = hi > 0 ? (hi + kBN - 1) / kBN : 0;
+  const int n_all = hi > 0 ? (hi + kBN - 1) / kBN : 0;
+  // Steps per group (the same for every group, so barriers pair up); step i
+  // of group g is tile g + NG i.  With NG = 2 and n_all odd, group 1's last
+  // tile lies past the keys: its loads read zeros or clamped rows and every
+  // score is masked.
+  const int n_tiles = (n_all + NG - 1) / NG;
+  auto gtile = [&](int i) { return grp + NG * i; };
 
   f32x16 acc[DB];
 #pragma unroll
@@ -350,8 +376,8 @@ void prefill_kernel(const PrefillParams p) {
   // Per-lane byte offset of this lane's first chunk; load u adds
   // u * (256 / CPR) rows.  Rows at or past kv_len fall outside the buffer
   // record and read as zero (their scores are masked), so no clamp is needed.
-  const int koff0 = (int)__umul24(tid / CPR, kst2) + 16 * (tid % CPR);
-  const int voff0 = (int)__umul24(tid / CPR, vst2) + 16 * (tid % CPR);
+  const int koff0 = (int)__umul24(gt / CPR, kst2) + 16 * (gt % CPR);
+  const int voff0 = (int)__umul24(gt / CPR, vst2) + 16 * (gt % CPR);
   constexpr int kRowsPerLoad = 256 / CPR;
   u32x4 kreg[LOADS], vreg[LOADS];
   // Paged streams: the same lane -> (row, chunk) mapping.  PG 1: page id per
@@ -370,25 +396,27 @@ void prefill_kernel(const PrefillParams p) {
     kpr.pshift = vpr.pshift = p.pshift;
     kpr.pmask = vpr.pmask = (1 << p.pshift) - 1;
     kpr.page_last = vpr.page_last = p.num_pages - 1;
-    kpr.row0 = vpr.row0 = tid / CPR;
+    kpr.row0 = vpr.row0 = gt / CPR;
+    kpr.tstep = vpr.tstep = NG;
     if constexpr (PG >= 2) {
       kpr.kv_len = vpr.kv_len = kv_len;
       kpr.last_idx = vpr.last_idx = max(kv_len - 1, 0) >> p.pshift;
-      kpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.k_st + 16 * (tid % CPR));
-      vpr.lane_off = (uint32_t)((tid / CPR) * 2 * p.v_st + 16 * (tid % CPR));
+      kpr.lane_off = (uint32_t)((gt / CPR) * 2 * p.k_st + 16 * (gt % CPR));
+      vpr.lane_off = (uint32_t)((gt / CPR) * 2 * p.v_st + 16 * (gt % CPR));
       kpr.cur = vpr.cur = 0;
       kpr.init_pool(p.num_pages);
       vpr.init_pool(p.num_pages);
     } else {
       kpr.kv_last = vpr.kv_last = max(kv_len - 1, 0);
-      kpr.col = vpr.col = 16 * (tid % CPR);
+      kpr.col = vpr.col = 16 * (gt % CPR);
     }
     if (n_tiles > 0) {
-      kpr.fetch_ids(0);
-      vpr.fetch_ids(0);
+      kpr.fetch_ids(gtile(0));
+      vpr.fetch_ids(gtile(0));
     }
   }
-  auto gload_k = [&](int tile) {
+  auto gload_k = [&](int step) {
+    const int tile = gtile(step);
     if constexpr (PAGED) {
       kpr.load(tile, kreg);
     } else {
@@ -399,7 +427,8 @@ void prefill_kernel(const PrefillParams p) {
                                                 krs, base + u * kRowsPerLoad * kst2, 0, 0));
     }
   };
-  auto gload_v = [&](int tile) {
+  auto gload_v = [&](int step) {
+    const int tile = gtile(step);
     if constexpr (PAGED) {
       vpr.load(tile, vreg);
     } else {
@@ -414,8 +443,8 @@ void prefill_kernel(const PrefillParams p) {
     if constexpr (PG >= 2) kpr.mask_tail(kreg);
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
-      const int cid = tid + 256 * u;
-      *reinterpret_cast<u32x4*>(&Ks[buf][(cid / CPR) * K_RS + 8 * (cid % CPR)]) = kreg[u];
+      const int cid = gt + 256 * u;
+      *reinterpret_cast<u32x4*>(&Ks[grp][buf][(cid / CPR) * K_RS + 8 * (cid % CPR)]) = kreg[u];
     }
   };
   // bf16: vreg is converted (convert_v) as soon as the step that loaded it
@@ -431,20 +460,20 @@ void prefill_kernel(const PrefillParams p) {
   };
   auto lstore_v = [&](int buf) {
     if constexpr (VH) {
-      if (lane == 0) vsc[buf][w] = v_s;
+      if (lane == 0) vsc[grp][buf][w] = v_s;
     } else if constexpr (PG >= 2) {
       vpr.mask_tail(vreg);
     }
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
-      const int cid = tid + 256 * u;
-      *reinterpret_cast<u32x4*>(&Vs[buf][(cid / CPR) * V_RS + 8 * (cid % CPR)]) = vreg[u];
+      const int cid = gt + 256 * u;
+      *reinterpret_cast<u32x4*>(&Vs[grp][buf][(cid / CPR) * V_RS + 8 * (cid % CPR)]) = vreg[u];
     }
   };
 
   // S^T = K Q^T for the two 32-key blocks of the K tile in Ks[buf].
   auto qk = [&](int buf, f32x16* s) {
-    const uint16_t* Kb = Ks[buf];
+    const uint16_t* Kb = Ks[grp][buf];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -506,8 +535,8 @@ void prefill_kernel(const PrefillParams p) {
       lstore_v(buf ^ 1);
       if (tile + 2 < n_tiles) gload_v(tile + 2);
     }
-    const int n0 = tile * kBN;
-    const uint16_t* Vb = Vs[buf];
+    const int n0 = gtile(tile) * kBN;
+    const uint16_t* Vb = Vs[grp][buf];
 
     // ---- scores of tile t: scale (c <= 0 only), mask, row max ----
     if (!POS) {
@@ -549,7 +578,7 @@ void prefill_kernel(const PrefillParams p) {
     // bf16: exponent offsets of the staging waves' V scales for tile t.
     float off[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
     float back[2][2] = {{1.f, 1.f}, {1.f, 1.f}};
-    if constexpr (VH) v_scale_offsets<CPR>(vsc[buf], g, e_acc, acc, off, back);
+    if constexpr (VH) v_scale_offsets<CPR>(vsc[grp][buf], g, e_acc, acc, off, back);
 
     // ---- S(t+1) on the MFMA pipe, interleaved with P(t) = 2^(s c - m) ----
 #ifdef FAT_PF_PRIO
@@ -558,7 +587,9 @@ void prefill_kernel(const PrefillParams p) {
     f32x16 s_nxt[2];
     if constexpr (HAS_NEXT) qk(buf ^ 1, s_nxt);
     const float cm = POS ? c : 1.f;
-    const float nm = -m_run;
+    // NG > 1: a row can have seen no key yet (its keys lie in the other
+    // group's tiles); m_run is then -inf and every score is -inf, so P = 0.
+    const float nm = (NG > 1 && m_run == -INFINITY) ? 0.f : -m_run;
     float lsq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
     u32x4 pf[2][2];
 #pragma unroll
@@ -602,6 +633,44 @@ void prefill_kernel(const PrefillParams p) {
   };
   for (int tile = 0; tile + 1 < n_tiles; ++tile) step(tile, std::true_type{});
   if (n_tiles > 0) step(n_tiles - 1, std::false_type{});
+
+  if constexpr (NG > 1) {
+    // Group 1 hands (O, m, l, e) to the wave of group 0 that owns the same
+    // rows, lane for lane, through the tile buffers; group 0 merges.
+    constexpr int NV = DB * 16 + 3;
+    static_assert(sizeof(Ks) >= 4 * NV * 64 * sizeof(float), "merge buffer");
+    float* xch = reinterpret_cast<float*>(&Ks[0][0][0]) + (w * NV) * 64 + lane;  // value e at xch[64 e]
+    __syncthreads();  // every wave is done with the tiles
+    if (grp == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[64 * (16 * db + r)] = acc[db][r];
+      xch[64 * (16 * DB)] = m_run;
+      xch[64 * (16 * DB + 1)] = l_run;
+      xch[64 * (16 * DB + 2)] = as_f32((u32)e_acc);
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = xch[64 * (16 * DB)];
+    const float l1 = xch[64 * (16 * DB + 1)];
+    const float mm = fmaxf(m_run, m1);
+    const float a0 = m_run == -INFINITY ? 0.f : fast_exp2(m_run - mm);
+    const float a1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mm);
+    l_run = l_run * a0 + l1 * a1;  // l is kept unscaled; only O carries 2^e_acc
+    float o0 = a0, o1 = a1;
+    if constexpr (VH) {
+      const int e1 = __builtin_amdgcn_readfirstlane((int)as_u32(xch[64 * (16 * DB + 2)]));
+      const int ee = max(e_acc, e1);
+      o0 *= as_f32((u32)(127 + e_acc - ee) << 23);
+      o1 *= as_f32((u32)(127 + e1 - ee) << 23);
+      e_acc = ee;
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db][r] = acc[db][r] * o0 + xch[64 * (16 * db + r)] * o1;
+  }
 
   // ---- epilogue: O = O^T / l, lane writes 4 consecutive dims per store ----
   const float l_tot = xor32<OpAdd>(l_run);
@@ -1015,12 +1084,12 @@ void prefill_pp_kernel(const PrefillParams p) {
 // ===========================================================================
 namespace {
 
-template <typename T, int D, bool CAUSAL, int PG>
+template <typename T, int D, bool CAUSAL, int PG, int NG>
 void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
   if (pos) {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true, PG>), grid, dim3(256), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true, PG, NG>), grid, dim3(256 * NG), 0, stream, prm);
   } else {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false, PG>), grid, dim3(256), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false, PG, NG>), grid, dim3(256 * NG), 0, stream, prm);
   }
 }
 
@@ -1033,41 +1102,70 @@ void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hip
   }
 }
 
+// Kernel families of the prefill launch.
+enum PrefillKind { PF_PINGPONG, PF_4WAVE, PF_4WAVE_SPLIT };
+
 template <typename T, int D, int PG>
-int launch_prefill_t(const fat::PrefillParams& prm, bool causal, bool pingpong, dim3 grid, hipStream_t stream) {
+int launch_prefill_t(const fat::PrefillParams& prm, bool causal, PrefillKind kind, dim3 grid, hipStream_t stream) {
   const bool pos = prm.scale_log2 > 0.f;
-  if (pingpong) {
+  if (kind == PF_PINGPONG) {
     if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
     else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
     return fat_host::launch_status("prefill_pp_kernel");
   }
-  if (causal) launch_prefill_c<T, D, true, PG>(prm, pos, grid, stream);
-  else launch_prefill_c<T, D, false, PG>(prm, pos, grid, stream);
+  if (kind == PF_4WAVE_SPLIT) {
+    if (causal) launch_prefill_c<T, D, true, PG, 2>(prm, pos, grid, stream);
+    else launch_prefill_c<T, D, false, PG, 2>(prm, pos, grid, stream);
+  } else {
+    if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, pos, grid, stream);
+    else launch_prefill_c<T, D, false, PG, 1>(prm, pos, grid, stream);
+  }
   return fat_host::launch_status("prefill_kernel");
 }
 
 bool valid_prefill_kernel(int kernel) {
-  return kernel == FAT_KERNEL_AUTO || kernel == FAT_KERNEL_PREFILL_PINGPONG || kernel == FAT_KERNEL_PREFILL_4WAVE;
+  return kernel == FAT_KERNEL_AUTO || kernel == FAT_KERNEL_PREFILL_PINGPONG || kernel == FAT_KERNEL_PREFILL_4WAVE ||
+         kernel == FAT_KERNEL_PREFILL_4WAVE_SPLIT;
 }
 
 // Kernel choice and grid shared by fat_prefill_varlen and fat_prefill_paged.
-// The 8-wave ping-pong kernel needs a grid of at least FAT_PF_PP_MIN
-// 256-row workgroups to fill the chip; smaller problems use the 4-wave,
-// 128-row kernel (twice the workgroups).  A non-AUTO `kernel` argument forces
-// one of them; with AUTO, FAT_PREFILL_KERNEL=pingpong|4wave overrides the
-// choice (tests exercise both kernels on every shape).
+// A workgroup's time is its chain of 64-key tiles, up to ceil(max_seqlen_k /
+// 64) for the longest query block; the launch ends with the longest chain on
+// the busiest CU.  The 8-wave ping-pong kernel (256 query rows, one
+// workgroup per CU) is the fastest per tile once its grid covers the 256 CUs:
+// non-causal grids of at least FAT_PF_PP_MIN_FULL workgroups, causal grids
+// (whose blocks differ in length) of more than FAT_PF_PP_MIN_CAUSAL.  Below
+// that the 4-wave kernel (128 rows, two workgroups per CU) runs, or its
+// 8-wave split form, whose two groups take alternate key tiles of one query
+// block and so halve its chain, when the 4-wave grid leaves CUs idle (at most
+// FAT_PF_SPLIT_MAX workgroups) and the chain is at least FAT_PF_SPLIT_TILES
+// tiles, or, causal, when it has at most 2 FAT_PF_SPLIT_MAX workgroups and
+// chains of at least FAT_PF_SPLIT_LONG tiles (the merge then costs less than
+// the balance gained).  A non-AUTO `kernel` argument forces one kernel; with
+// AUTO, FAT_PREFILL_KERNEL=pingpong|4wave|4wave_split overrides the choice (tests
+// exercise every kernel on every shape).
 template <int PG>
-int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int dtype, int D, bool causal, float softmax_scale,
-                   int kernel, const char* who, hipStream_t stream) {
-  const int64_t nqb_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM;
-  bool pingpong = nqb_pp * prm.B * prm.H >= FAT_PF_PP_MIN;
+int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
+                   float softmax_scale, int kernel, const char* who, hipStream_t stream) {
+  const int64_t heads = (int64_t)prm.B * prm.H;
+  const int64_t n_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM * heads;
+  const int64_t n_4w = (max_seqlen_q + fat::kBM - 1) / fat::kBM * heads;
+  const int64_t chain = (max_seqlen_k + fat::kBN - 1) / fat::kBN;
+  PrefillKind kind = PF_4WAVE;
+  if (causal ? n_pp > FAT_PF_PP_MIN_CAUSAL : n_pp >= FAT_PF_PP_MIN_FULL) kind = PF_PINGPONG;
+  else if ((n_4w <= FAT_PF_SPLIT_MAX && chain >= FAT_PF_SPLIT_TILES) ||
+           (causal && n_4w <= 2 * FAT_PF_SPLIT_MAX && chain >= FAT_PF_SPLIT_LONG))
+    kind = PF_4WAVE_SPLIT;
   if (kernel != FAT_KERNEL_AUTO) {
-    pingpong = kernel == FAT_KERNEL_PREFILL_PINGPONG;
+    kind = kernel == FAT_KERNEL_PREFILL_PINGPONG ? PF_PINGPONG
+           : kernel == FAT_KERNEL_PREFILL_4WAVE  ? PF_4WAVE
+                                                 : PF_4WAVE_SPLIT;
   } else if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
-    if (!strcmp(force, "pingpong")) pingpong = true;
-    else if (!strcmp(force, "4wave")) pingpong = false;
+    if (!strcmp(force, "pingpong")) kind = PF_PINGPONG;
+    else if (!strcmp(force, "4wave")) kind = PF_4WAVE;
+    else if (!strcmp(force, "4wave_split")) kind = PF_4WAVE_SPLIT;
   }
-  const int bm = pingpong ? fat::kPBM : fat::kBM;
+  const int bm = kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
   prm.nqb = (max_seqlen_q + bm - 1) / bm;
   prm.scale_log2 = softmax_scale * fat::kLog2e;
   const int64_t n = (int64_t)prm.nqb * prm.B * prm.H;
@@ -1077,11 +1175,11 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int dtype, int D, 
   }
   const dim3 grid((unsigned)n);
   if (dtype == FAT_DTYPE_F16) {
-    return D == 128 ? launch_prefill_t<fat::F16, 128, PG>(prm, causal, pingpong, grid, stream)
-                    : launch_prefill_t<fat::F16, 64, PG>(prm, causal, pingpong, grid, stream);
+    return D == 128 ? launch_prefill_t<fat::F16, 128, PG>(prm, causal, kind, grid, stream)
+                    : launch_prefill_t<fat::F16, 64, PG>(prm, causal, kind, grid, stream);
   }
-  return D == 128 ? launch_prefill_t<fat::BF16, 128, PG>(prm, causal, pingpong, grid, stream)
-                  : launch_prefill_t<fat::BF16, 64, PG>(prm, causal, pingpong, grid, stream);
+  return D == 128 ? launch_prefill_t<fat::BF16, 128, PG>(prm, causal, kind, grid, stream)
+                  : launch_prefill_t<fat::BF16, 64, PG>(prm, causal, kind, grid, stream);
 }
 
 }  // namespace
@@ -1117,8 +1215,8 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
     return FAT_E_UNSUPPORTED;
   }
   if (!valid_prefill_kernel(a->kernel)) {
-    fat_host::set_error("fat_prefill_varlen: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1) or "
-                        "_PREFILL_4WAVE (2), got %d", a->kernel);
+    fat_host::set_error("fat_prefill_varlen: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
+                        "_PREFILL_4WAVE (2) or _PREFILL_4WAVE_SPLIT (3), got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
@@ -1168,8 +1266,8 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = a->num_heads / a->num_kv_heads;
-  return launch_prefill<0>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
-                           "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
+  return launch_prefill<0>(prm, a->max_seqlen_q, a->max_seqlen_k, a->dtype, D, a->causal != 0, a->softmax_scale,
+                           a->kernel, "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
 }
 
 extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_ptr) {
@@ -1197,8 +1295,8 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     return FAT_E_UNSUPPORTED;
   }
   if (!valid_prefill_kernel(a->kernel)) {
-    fat_host::set_error("fat_prefill_paged: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1) or "
-                        "_PREFILL_4WAVE (2), got %d", a->kernel);
+    fat_host::set_error("fat_prefill_paged: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
+                        "_PREFILL_4WAVE (2) or _PREFILL_4WAVE_SPLIT (3), got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
@@ -1275,12 +1373,13 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     else if (!strcmp(force, "wide")) off32 = false;
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const int64_t kv_bound = (int64_t)a->max_pages * P;  // longest context the table can hold
   if (uniform && off32)
-    return launch_prefill<3>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
-                             "fat_prefill_paged", stream);
+    return launch_prefill<3>(prm, a->max_seqlen_q, kv_bound, a->dtype, D, a->causal != 0, a->softmax_scale,
+                             a->kernel, "fat_prefill_paged", stream);
   if (uniform)
-    return launch_prefill<2>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
-                             "fat_prefill_paged", stream);
-  return launch_prefill<1>(prm, a->max_seqlen_q, a->dtype, D, a->causal != 0, a->softmax_scale, a->kernel,
-                           "fat_prefill_paged", stream);
+    return launch_prefill<2>(prm, a->max_seqlen_q, kv_bound, a->dtype, D, a->causal != 0, a->softmax_scale,
+                             a->kernel, "fat_prefill_paged", stream);
+  return launch_prefill<1>(prm, a->max_seqlen_q, kv_bound, a->dtype, D, a->causal != 0, a->softmax_scale,
+                           a->kernel, "fat_prefill_paged", stream);
 }

@@ -62,7 +62,10 @@ enum fat_kernel {
   FAT_KERNEL_DECODE_VALU = 1,      /* one query per sequence (q_len <= 1)     */
   FAT_KERNEL_DECODE_MFMA = 2,      /* any cache dtype and q_len               */
   FAT_KERNEL_PREFILL_PINGPONG = 1, /* 8 waves, 256 query rows per workgroup   */
-  FAT_KERNEL_PREFILL_4WAVE = 2     /* 4 waves, 128 query rows per workgroup   */
+  FAT_KERNEL_PREFILL_4WAVE = 2,    /* 4 waves, 128 query rows per workgroup   */
+  FAT_KERNEL_PREFILL_4WAVE_SPLIT = 3 /* 8 waves, 128 query rows: two 4-wave
+                                        groups take alternate key tiles and
+                                        merge (m, l, O) at the end          */
 };
 
 /* Error codes. */

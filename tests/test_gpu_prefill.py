@@ -22,7 +22,7 @@ DEV = "cuda"
 ODD_LENS = [1, 17, 255, 1000]
 
 
-@pytest.fixture(params=["auto", "pingpong", "4wave"])
+@pytest.fixture(params=["auto", "pingpong", "4wave", "4wave_split"])
 def kernel(request, monkeypatch):
     """Run the test with the library's automatic choice and with each of the
     two prefill kernels forced (8-wave ping-pong, 4-wave), whatever the shape."""

@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(params=["auto", "pingpong", "4wave"])
+@pytest.fixture(params=["auto", "pingpong", "4wave", "4wave_split"])
 def kernel(request, monkeypatch):
     monkeypatch.setenv("FAT_PREFILL_KERNEL", request.param)
     return request.param

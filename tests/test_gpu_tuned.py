@@ -62,7 +62,7 @@ def test_multi_token_decode_kernel_choice():
         paged_decode_attention_multi(q, cache, config={"split_k": 2, "kernel": "valu"})
 
 
-@pytest.mark.parametrize("kern", ["pingpong", "4wave"])
+@pytest.mark.parametrize("kern", ["pingpong", "4wave", "4wave_split"])
 def test_prefill_kernel_config_equals_env_forcing(kern, monkeypatch):
     label = f"prefill kernel={kern}"
     print(label, flush=True)
@@ -104,7 +104,7 @@ def test_store_routes_config_none_launches(tmp_path, monkeypatch):
     lens = [1, 255, 1000]
     qp, k, v, cu = make_varlen(lens, 32, 8, 128, torch.bfloat16, seed=22, device=DEV)
     psig = at.prefill_signature(3, 32, 8, 128, 1000, 1000, True)
-    for kern in ("pingpong", "4wave"):
+    for kern in ("pingpong", "4wave", "4wave_split"):
         at.save_best("prefill", psig, {"kernel": kern})
         got = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True)
         want = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True, config={"kernel": kern})
