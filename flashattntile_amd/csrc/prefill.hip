@@ -75,8 +75,8 @@ constexpr int kBufFlags = 0x00020000;
 // Rows of a K or V stream read through the page table.  A lane loads LOADS
 // 16-byte chunks per tile, at rows row0 + u * RPL (u < LOADS) of the tile and
 // byte column `col`.  The page ids a load needs are fetched by the previous
-// load of the same stream (tiles are loaded in increasing order), so the
-// table lookup latency hides behind a whole tile of compute.
+// load of the same stream (a stream loads every tstep-th tile, in increasing
+// order), so the table lookup latency hides behind a whole tile of compute.
 template <int LOADS, int RPL>
 struct PagedRows {
   const uint8_t* base;  // cache + this KV head's offset
@@ -96,7 +96,8 @@ struct PagedRows {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) pg[u] = min(max(pt_row[row_of(tile, u) >> pshift], 0), page_last);
   }
-  // The chunks of `tile` (its ids already in pg), then the ids of tile + 1.
+  // The chunks of `tile` (its ids already in pg), then the ids of the
+  // stream's next tile, tile + tstep.
   __device__ __forceinline__ void load(int tile, u32x4 (&dst)[LOADS]) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
