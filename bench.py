@@ -30,6 +30,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -151,10 +152,12 @@ def _time_steps(fn, steps, warmup, stream):
 
 
 def _time_steps_flushed(fn, steps, warmup, stream, flush):
-    """Each step timed by its own event pair after a 512 MB read that evicts
-    the Infinity Cache (for working sets the MALL could otherwise hold).  The
-    flush only reads (a max-reduction into 8 bytes), so it leaves no dirty
-    lines for the timed kernel to write back."""
+    """Median over steps, each timed by its own event pair after a 512 MB
+    read that evicts the Infinity Cache (for working sets the MALL could
+    otherwise hold).  The flush only reads (a max-reduction into 8 bytes), so
+    it leaves no dirty lines for the timed kernel to write back.  The median,
+    not the mean: one launch delayed by the system (seen once at 0.7 ms for a
+    30 us launch) would otherwise dominate a row of ~20 samples."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -169,7 +172,7 @@ def _time_steps_flushed(fn, steps, warmup, stream, flush):
         e1.record(stream)
         evs.append((e0, e1))
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / steps
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
 
 
 def _time_cpu(fn, budget_s, max_reps=21):
@@ -378,7 +381,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     steps = max(20, args.steps // 4)
     if pool_bytes * copies < 2 * MALL_BYTES:
         ms = _time_steps_flushed(step, steps, 5, stream, flush)
-        timing = "per-launch events after a 512 MB cache flush"
+        timing = "median of per-launch events, each after a 512 MB cache flush"
     else:
         ms = _time_steps(step, steps, 5, stream)
         timing = f"back-to-back, {copies} pool copies alternating"
