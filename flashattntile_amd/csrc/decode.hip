@@ -119,6 +119,35 @@ struct UnitRegs {
   float vsc[NI];
 };
 
+// 16 bytes of int8 or OCP e4m3 K as their exact values in fp16 (8 packed
+// pairs).  With fp16 queries both decode kernels stage K this way and apply
+// k_scale to the fp32 scores, as the reference's quantised kernel does
+// (kernels/decode.py:419-429: k = float(x) * k_scale, scores in fp32):
+// 5 (int8) or 2 (fp8) instructions per 4 elements instead of 11 or 8 for
+// round_to_fp16(float(x) * scale).  V keeps that per-element dequantisation:
+// folding v_scale into P would round P after a scale that differs per page,
+// and pages whose scales differ by 2^15 or more (two can share a 32-key
+// block) would leave the smaller one's P in fp16's subnormal range.
+template <int KV>
+__device__ __forceinline__ void k8_exact_f16(const u32x4& raw, u32 (&out)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (KV == KV_I8) {
+      // fp16 bits 0x6400 | u are 1024 + u exactly (u = x + 128, the byte with
+      // its sign bit flipped); adding -1152 leaves x.
+      const u32 u = raw[j] ^ 0x80808080u;
+      const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+      out[2 * j] = __builtin_bit_cast(
+          u32, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + bias);
+      out[2 * j + 1] = __builtin_bit_cast(
+          u32, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + bias);
+    } else {  // OCP e4m3 -> fp16 is exact
+      out[2 * j] = __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[j], 1.0f, false));
+      out[2 * j + 1] = __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[j], 1.0f, true));
+    }
+  }
+}
+
 template <typename QT, int KV, int D, int HG, int NW>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
   using Gm = Geom<KV, D>;
@@ -203,6 +232,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     }
   };
 
+  // FOLD: exact 8-bit K and k_scale on the scores (k8_exact_f16).
+  constexpr bool FOLD = KV != KV_SAME && std::is_same<QT, F16>::value;
   // Dequantise 16 bytes of 8-bit K/V into EPL/2 packed QT pairs:
   // round_to_QT(float(x) * scale).
   auto deq_pairs = [&](const u32x4& raw, float sc, u32* out) {
@@ -252,6 +283,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
       if constexpr (KV == KV_SAME) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) kw[j] = cur.k[i][j];
+      } else if constexpr (FOLD) {
+        k8_exact_f16<KV>(cur.k[i], kw);
       } else {
         deq_pairs(cur.k[i], cur.ksc[i], kw);
       }
@@ -260,7 +293,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < QW; ++j) s = Pair<QT>::dot2(qv[g][j], kw[j], s);
-        part[g * NI + i] = s;
+        part[g * NI + i] = FOLD ? s * cur.ksc[i] : s;  // load i's rows share one page
       }
     }
     transpose_reduce<LPR, NV>(part, c);
@@ -525,8 +558,18 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
       }
     }
   };
+  // FOLD (8-bit cache, fp16 queries): exact 8-bit K and k_scale on the
+  // scores (k8_exact_f16).
+  constexpr bool FOLD = KV != KV_SAME && std::is_same<QT, F16>::value;
   // Store one raw chunk as QT elements at dst (EPC of them): a copy for
-  // fp16/bf16 caches, round_to_QT(float(x) * scale) for 8-bit ones.
+  // fp16/bf16 caches, round_to_QT(float(x) * scale) for 8-bit ones, or
+  // (put_exact, FOLD K) the exact 8-bit values.
+  auto put_exact = [&](uint16_t* dst, const u32x4& raw) {
+    u32 o[8];
+    k8_exact_f16<KV>(raw, o);
+    *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
+  };
   auto put = [&](uint16_t* dst, const u32x4& raw, float sc) {
     if constexpr (KV == KV_SAME) {
       *reinterpret_cast<u32x4*>(dst) = raw;
@@ -576,10 +619,16 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
   auto compute = [&](Raw& R, int blk, int nxt) {
     // K(blk) and V(blk) into this wave's LDS tiles (row = key, columns =
     // head dims), then R is free for the next block's loads.
+    float ck[NLD];  // FOLD: score factor (softmax scale times k_scale) per load
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int row = i * RPL + lrow;
-      put(&Kt[row * K_RS + lcol * EPC], R.k[i], R.ksc[i]);
+      if constexpr (FOLD) {
+        ck[i] = c * R.ksc[i];
+        put_exact(&Kt[row * K_RS + lcol * EPC], R.k[i]);
+      } else {
+        put(&Kt[row * K_RS + lcol * EPC], R.k[i], R.ksc[i]);
+      }
       put(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
     }
     if (nxt < n_blocks) fetch(R, nxt);
@@ -600,7 +649,9 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb + (r & 3) + 4 * g + 8 * (r >> 2);
-      const float x = key < my_end ? s[r] * c : -INFINITY;
+      // key row 8 (r >> 2) + (r & 3) + 4g of the block: load (r >> 2) * 8 / RPL
+      const float cr = FOLD ? ck[(r >> 2) * 8 / RPL] : c;
+      const float x = key < my_end ? s[r] * cr : -INFINITY;
       s[r] = x;
       mx = fmaxf(mx, x);
     }

@@ -15,7 +15,7 @@ import math
 import pytest
 import torch
 
-from _parity import assert_parity, make_paged, make_query
+from _parity import assert_parity, make_paged, make_query, ulp
 from flashattntile_amd import PagedKVCache, paged_decode_attention, paged_decode_attention_fp8
 from flashattntile_amd.kernels.decode import paged_decode_launch
 from oracle import quant_ref
@@ -130,6 +130,51 @@ def test_quant_decode_matches_dequantized_oracle(mode, qdtype, d, h, hk, split_k
     torch.cuda.synchronize()
     assert out.dtype == qdtype
     assert_parity(out, ref, label=label)
+
+
+@pytest.mark.parametrize("order", ["random", "growing"])
+@pytest.mark.parametrize("split_k", [1, 4])
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+def test_quant_decode_extreme_page_scales(mode, split_k, order, decode_kernel):
+    """Per-page V magnitudes from 1e-6 to 4e4 (K from 1e-2 to 10, logits
+    with a standard deviation near 10), so the (page, KV head) scales span
+    ten decades and neighbouring pages (which may share a 32-key block)
+    differ by up to that much; "growing" orders each sequence's pages by
+    increasing V magnitude.  With fp16 queries the kernels apply k_scale to
+    the fp32 scores, as the reference's quantised kernel does
+    (kernels/decode.py:419-429), so the oracle here dequantises to fp32, as
+    the reference's own numerics test does (tests/test_numerics.py:152):
+    at these logits the fp16 rounding of a dequantised K alone moves the
+    softmax by 0.5 %.  2e-3 relative to each output row's magnitude beyond
+    the final fp16 rounding."""
+    label = f"quant {decode_kernel} {mode} extreme page scales {order} sk{split_k}"
+    print(label, flush=True)
+    lens = [700, 4096, 129, 33]
+    k, v, pt, sl = make_paged(lens, 8, 128, 16, torch.float32, seed=41, device="cpu", poison=False)
+    g = torch.Generator().manual_seed(42)
+    n = k.shape[0]
+    v_exp = torch.rand(n, generator=g) * 10.0 - 6.0  # log10 of the page's V magnitude, 1e-6 .. 1e4
+    k_exp = torch.rand(n, generator=g) * 3.0 - 2.0
+    if order == "growing":  # page j of each sequence gets a larger V magnitude than page j - 1
+        for b, ln in enumerate(lens):
+            pages = pt[b, : -(-ln // 16)].long()
+            v_exp[pages] = torch.linspace(-6.0, 4.0, len(pages))
+    v = v * torch.pow(10.0, v_exp).view(n, 1, 1, 1) * 4.0 / 4.5  # |v| stays below fp16 max after dequant
+    k = k * torch.pow(10.0, k_exp).view(n, 1, 1, 1)
+    qk, sk = quant_ref.quantize_pages(k, mode)
+    qv, sv = quant_ref.quantize_pages(v, mode)
+    q = make_query(len(lens), 32, 128, torch.float16, seed=43, device=DEV)
+    cache = PagedKVCache(qk.to(DEV), qv.to(DEV), pt.to(DEV), sl.to(DEV), 16)
+    ref = ref_attention_paged(q.cpu().float(), quant_ref.dequantize_pages(qk, sk, torch.float32),
+                              quant_ref.dequantize_pages(qv, sv, torch.float32), pt, sl, return_fp32=True)
+    out = paged_decode_attention_fp8(q, cache, {"k": sk.to(DEV), "v": sv.to(DEV)}, config={"split_k": split_k})
+    torch.cuda.synchronize()
+    o32, r32 = out.float().cpu(), ref.float()
+    scale = r32.abs().amax(dim=-1, keepdim=True).clamp_min(1.0)
+    rounding = 0.5 * ulp(torch.maximum(o32.abs(), r32.abs()), torch.float16)
+    excess = ((o32 - r32).abs() - rounding) / scale
+    print(f"{label}: max relative error beyond rounding {excess.max().item():.3e}", flush=True)
+    assert torch.isfinite(o32).all() and excess.max().item() <= 2e-3, label
 
 
 def test_permuted_pool_is_bit_identical():
