@@ -559,14 +559,29 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
     }
   };
   // FOLD (8-bit cache, fp16 queries): exact 8-bit K and k_scale on the
-  // scores (k8_exact_f16).
+  // scores (k8_exact_f16).  int8 V as x * fp16(v_scale), one packed fp16
+  // multiply per pair (FOLD_V): within one fp16 ulp of round_to_fp16(
+  // float(x) * v_scale) (the scale's own rounding to fp16 is the second
+  // rounding; a scale below fp16's normal range, 6.1e-5, can be off by up to
+  // 3e-8, i.e. a V error below 4e-6), inside the dequantise-then-attend
+  // tolerance.  fp8 V keeps the fp32 dequantise, which measured faster there.
   constexpr bool FOLD = KV != KV_SAME && std::is_same<QT, F16>::value;
+  constexpr bool FOLD_V = FOLD && KV == KV_I8;
   // Store one raw chunk as QT elements at dst (EPC of them): a copy for
   // fp16/bf16 caches, round_to_QT(float(x) * scale) for 8-bit ones, or
   // (put_exact, FOLD K) the exact 8-bit values.
   auto put_exact = [&](uint16_t* dst, const u32x4& raw) {
     u32 o[8];
     k8_exact_f16<KV>(raw, o);
+    *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<u32x4*>(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
+  };
+  auto put_scaled = [&](uint16_t* dst, const u32x4& raw, float sc) {
+    u32 o[8];
+    k8_exact_f16<KV>(raw, o);
+    const f16x2 s2 = {(f16)sc, (f16)sc};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = __builtin_bit_cast(u32, __builtin_bit_cast(f16x2, o[j]) * s2);
     *reinterpret_cast<u32x4*>(dst) = u32x4{o[0], o[1], o[2], o[3]};
     *reinterpret_cast<u32x4*>(dst + 8) = u32x4{o[4], o[5], o[6], o[7]};
   };
@@ -629,7 +644,11 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
       } else {
         put(&Kt[row * K_RS + lcol * EPC], R.k[i], R.ksc[i]);
       }
-      put(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
+      if constexpr (FOLD_V) {
+        put_scaled(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
+      } else {
+        put(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
+      }
     }
     if (nxt < n_blocks) fetch(R, nxt);
     wave_lds_fence();
