@@ -175,11 +175,16 @@ def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: i
     ``total_pages``) is spread over about one workgroup per CU with at most
     ``max_split`` partitions -- the same launch as :func:`decode_split_k` --
     or up to 64 when every partition still holds at least 256 pages.  A
-    skewed batch gets many small partitions (about 16 workgroups per CU, up to
-    64 partitions), so the long sequences are streamed by many workgroups and
-    the dispatcher balances the uneven rest.  Both regimes were measured on
-    MI355X (32/8 heads, D128, page 16: the B x ctx sweep and 64 log-uniform
-    lengths in [16, 65536]).
+    skewed batch gets about 4 workgroups per CU (up to 64 partitions), so
+    the long sequences are streamed by many workgroups and the dispatcher
+    balances the uneven rest, and an odd split_k: workgroups go to the 8 XCDs
+    round-robin with the partition index fastest, so with an even split_k the
+    only non-empty partition of every short sequence (partition 0) lands on
+    half of the XCDs or fewer.  Both regimes were measured on MI355X (32/8
+    heads, D128, page 16: the B x ctx sweep; 64 log-uniform lengths in [16,
+    65536], 2 x 65536 + 30 x 512 and 128 log-uniform lengths in [16, 16384],
+    where this rule with 4-wave workgroups ran 533 / 176 / 324 us against 674
+    / 497 / 334 us for 16 workgroups per CU and 8 waves).
     """
     group = max(1, num_heads // max(1, num_kv_heads))
     rows = group * max(1, int(q_len))  # (query head, token) rows per KV head
@@ -188,7 +193,7 @@ def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: i
     max_pages = max(1, int(max_pages))
     total_pages = max(1, int(total_pages))
     skewed = is_ragged(batch, max_pages, total_pages)
-    target_wgs = 16 * num_cus if skewed else num_cus
+    target_wgs = 4 * num_cus if skewed else num_cus
     chunk = max(min_pages_per_split, math.ceil(total_pages * groups / target_wgs))
     # Partitions of at least 256 pages may number up to 64: the merge is then
     # negligible and one long sequence still reaches every CU (B1 ctx131072:
@@ -198,6 +203,10 @@ def decode_partition(batch: int, num_heads: int, num_kv_heads: int, max_pages: i
     if split > cap:
         split = cap
         chunk = math.ceil(max_pages / split)
+    if skewed and split > 1:
+        if split % 2 == 0:
+            split = split + 1 if split < cap else split - 1
+        chunk = math.ceil(max_pages / split)  # equal partitions of the longest sequence
     return int(max(1, split)), int(chunk)
 
 

@@ -64,10 +64,17 @@ def test_partition_heuristic():
     assert at.decode_partition(1, 32, 8, 1024, 1024) == (16, 64)
     # partitions of >= 256 pages: up to 64 of them, so B1 ctx131072 fills the CUs
     assert at.decode_partition(1, 32, 8, 8192, 8192) == (32, 256)
-    # skewed batch: small partitions (~16 workgroups per CU), split covers the longest sequence
+    # skewed batch: ~4 workgroups per CU, an odd split covering the longest sequence
     split, chunk = at.decode_partition(64, 32, 8, 4096, 40019)
-    assert chunk == -(-40019 * 8 // (16 * 256)) and split == -(-4096 // chunk)
-    assert split * chunk >= 4096 and split <= 64
+    c0 = -(-40019 * 8 // (4 * 256))
+    s0 = -(-4096 // c0)
+    assert split == (s0 + 1 if s0 % 2 == 0 else s0) and chunk == -(-4096 // split)
+    assert split % 2 == 1 and split * chunk >= 4096 and split <= 64
+    # the bench's 64 log-uniform lengths and 2 x 65536 + 30 x 512 (measured best at 13 and 57 partitions)
+    assert at.decode_partition(64, 32, 8, 3998, 40049) == (13, 308)
+    assert at.decode_partition(32, 32, 8, 4096, 9152) == (57, 72)
+    # at the 64-partition cap an even split steps down (one 100000-page sequence among 15 of one page)
+    assert at.decode_partition(16, 32, 8, 100000, 100015) == (63, 1588)
 
 
 # ---------------------------------------------------------------------------
