@@ -20,7 +20,8 @@ that is the untuned launch spelled out, keep the untuned entry.
 Shapes (synthetic, seeded, N(0, 1) values, randomly permuted page pools):
 decode fp16 32/8 heads D128 P16 for B in {1, 8, 32, 128} x ctx in {128,
 1024, 4096, 16384}; int8 and fp8 decode B128 ctx16384; B1 ctx131072; MQA
-32/1 B32 ctx4096; 4-token decode B32 ctx4096; causal prefill of one fp16
+32/1 B32 ctx4096; 4-token decode B32 ctx4096; bf16 and D64 decode B32
+ctx4096; causal prefill of one fp16
 sequence, L in {512, ..., 8192}; paged prefill L8192 at page size 16.
 """
 
@@ -42,23 +43,27 @@ from .kernels.prefill import paged_prefill_launch, prefill_launch
 from .paging import PagedKVCache
 from .quant import quantize_cache
 
+# (batch, ctx, query heads, KV heads, quantised dtype, q_len[, head_dim, dtype])
 DECODE_SHAPES = [(b, ctx, 32, 8, None, 1) for b in (1, 8, 32, 128) for ctx in (128, 1024, 4096, 16384)] + [
     (128, 16384, 32, 8, torch.int8, 1),
     (128, 16384, 32, 8, torch.float8_e4m3fn, 1),
     (1, 131072, 32, 8, None, 1),
     (32, 4096, 32, 1, None, 1),
     (32, 4096, 32, 8, None, 4),
+    (32, 4096, 32, 8, None, 1, 128, torch.bfloat16),
+    (32, 4096, 32, 8, None, 1, 64, torch.float16),
 ]
 PREFILL_LENS = (512, 1024, 2048, 4096, 8192)
 D, P = 128, 16
 
 
-def _paged_cache(batch: int, ctx: int, hkv: int, gen: torch.Generator, device) -> PagedKVCache:
+def _paged_cache(batch: int, ctx: int, hkv: int, gen: torch.Generator, device, d: int = D,
+                 dtype=torch.float16) -> PagedKVCache:
     pages = -(-ctx // P)
     num_pages = batch * pages
     perm = torch.randperm(num_pages, generator=gen, device=device).to(torch.int32)
-    k = torch.randn(num_pages, P, hkv, D, generator=gen, device=device, dtype=torch.float16)
-    v = torch.randn(num_pages, P, hkv, D, generator=gen, device=device, dtype=torch.float16)
+    k = torch.randn(num_pages, P, hkv, d, generator=gen, device=device, dtype=torch.float32).to(dtype)
+    v = torch.randn(num_pages, P, hkv, d, generator=gen, device=device, dtype=torch.float32).to(dtype)
     return PagedKVCache(k_cache=k, v_cache=v, page_table=perm.view(batch, pages).contiguous(),
                         seq_lens=torch.full((batch,), ctx, dtype=torch.int32, device=device), page_size=P)
 
@@ -95,22 +100,24 @@ def _pick(problem: dict, rows: list[dict], default: dict, keys, min_gain: float,
 
 
 def tune_decode(device, out_path, min_gain: float) -> None:
-    for (batch, ctx, hq, hkv, qdt, q_len) in DECODE_SHAPES:
+    for shape in DECODE_SHAPES:
+        batch, ctx, hq, hkv, qdt, q_len = shape[:6]
+        d, dtype = shape[6:] if len(shape) > 6 else (D, torch.float16)
         gen = torch.Generator(device=device).manual_seed(batch * 7919 + ctx)
-        pool_bytes = batch * ctx * hkv * D * 2 * (1 if qdt is not None else 2)
+        pool_bytes = batch * ctx * hkv * d * 2 * (1 if qdt is not None else 2)
         caches, scale_list = [], []
         for _ in range(_copies(pool_bytes)):
-            cache = _paged_cache(batch, ctx, hkv, gen, device)
+            cache = _paged_cache(batch, ctx, hkv, gen, device, d, dtype)
             scales = None
             if qdt is not None:
                 cache, scales = quantize_cache(cache, "int8" if qdt == torch.int8 else "fp8")
             caches.append(cache)
             scale_list.append(None if scales is None else {"k": scales.k, "v": scales.v})
         cache = caches[0]
-        shape = (batch, q_len, hq, D) if q_len > 1 else (batch, hq, D)
-        q = torch.randn(*shape, generator=gen, device=device, dtype=torch.float16)
+        qshape = (batch, q_len, hq, d) if q_len > 1 else (batch, hq, d)
+        q = torch.randn(*qshape, generator=gen, device=device, dtype=torch.float32).to(dtype)
         out = torch.empty_like(q)
-        ws = torch.empty(_hip.decode_workspace_bytes(batch * q_len, hq, D, 64), dtype=torch.uint8, device=device)
+        ws = torch.empty(_hip.decode_workspace_bytes(batch * q_len, hq, d, 64), dtype=torch.uint8, device=device)
         max_pages = -(-ctx // P)
         total = batch * max_pages
         quantized = qdt is not None
@@ -123,15 +130,15 @@ def tune_decode(device, out_path, min_gain: float) -> None:
 
         def run(cfg):
             i = turn[0] = (turn[0] + 1) % len(caches)
-            paged_decode_launch(q, caches[i], D ** -0.5, cfg["split_k"], out=out, workspace=ws,
+            paged_decode_launch(q, caches[i], d ** -0.5, cfg["split_k"], out=out, workspace=ws,
                                 scales=scale_list[i], waves_per_group=cfg["num_warps"],
                                 pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"])
 
-        nbytes = bytes_decode_paged([ctx] * batch, hq * q_len, hkv, D, kv_elem_bytes=1 if quantized else 2,
+        nbytes = bytes_decode_paged([ctx] * batch, hq * q_len, hkv, d, kv_elem_bytes=1 if quantized else 2,
                                     page_size=P, quantized=quantized)
-        sig = decode_signature(batch, hq, hkv, D, P, ctx, total, cache.k_cache.dtype, q_len)
+        sig = decode_signature(batch, hq, hkv, d, P, ctx, total, cache.k_cache.dtype, q_len)
         problem = {"kind": "decode", "signature": sig, "runner": run, "bytes": nbytes,
-                   "flops": 4 * batch * hq * q_len * D * ctx}
+                   "flops": 4 * batch * hq * q_len * d * ctx}
         rows = autotune(problem, cands, save=False, timer=_timer)
         cfg, metrics = _pick(problem, rows, default, list(default), min_gain)
         save_best("decode", sig, cfg, metrics, path=out_path)
