@@ -349,7 +349,8 @@ def cpu_baseline_decode(budget_s=12.0):
 # ---------------------------------------------------------------------------
 # Every BASELINE.json configuration
 # ---------------------------------------------------------------------------
-def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, quant=None, cpu_seqs=2):
+def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, quant=None, cpu_seqs=2,
+                dtype=torch.float16):
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
@@ -359,7 +360,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     kv_elem = 1 if quant else 2
     pool_bytes = sum(lens) * hkv * d * 2 * kv_elem
     copies = 1 if pool_bytes >= 2 * MALL_BYTES else 2
-    q, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, torch.float16, seed=11,
+    q, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, dtype, seed=11,
                                                              device=device, copies=copies, quant=quant)
     maxp = table.shape[1]
     total_pages = sum(math.ceil(n / page) for n in lens)
@@ -716,7 +717,8 @@ def all_configs(args, device):
     for B in (1, 8, 32, 128):
         for ctx in (128, 1024, 4096, 16384):
             emit(_decode_row(f"decode fp16 B{B} ctx{ctx}", [ctx] * B, 32, 8, 128, 16, device, args, flush))
-    emit(_decode_row("decode bf16 B32 ctx4096", [4096] * 32, 32, 8, 128, 16, device, args, flush))
+    emit(_decode_row("decode bf16 B32 ctx4096", [4096] * 32, 32, 8, 128, 16, device, args, flush,
+                     dtype=torch.bfloat16))
     # prefill fp16 / bf16, L in 512..8192 and the mixed pack
     g = torch.Generator().manual_seed(2024)
     mixed = torch.randint(1, 4097, (8,), generator=g).tolist()
