@@ -20,6 +20,9 @@
 //   * int8/fp8 pages are dequantised in registers as
 //     round_to_q_dtype(float(x) * scale), the reference's own
 //     dequantise-then-attend semantics (flashattn_tile/quant.py:145-161);
+//     with fp16 queries K is staged exact and k_scale multiplies the fp32
+//     scores (the reference's quantised kernel, kernels/decode.py:419-429),
+//     and the MFMA decode forms int8 V as x * fp16(scale) (k8_exact_f16);
 //   * with split_k > 1 each workgroup writes (acc, m, l) for its partition
 //     and a second kernel merges the partitions by log-sum-exp;
 //   * multi-token decode (q_len = T > 1, e.g. speculative verification) runs

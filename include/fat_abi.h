@@ -103,10 +103,14 @@ enum fat_status {
  * split_k * pages_per_split).  With split_k > 1 the partitions are merged by
  * a log-sum-exp reduction through `workspace`, which must hold
  * fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k) bytes
- * (it may be NULL when split_k == 1).  int8/fp8 pages are dequantised as
- * round_to_q_dtype(float(x) * scale) before the fp32 attention, exactly as
+ * (it may be NULL when split_k == 1).  int8/fp8 pages: with bf16 queries
+ * K and V are dequantised as round_to_bf16(float(x) * scale), as
  * dequantize_kv_pages (flashattn_tile/quant.py:145-161) followed by the fp32
- * reference does.
+ * reference does.  With fp16 queries k_scale multiplies the fp32 scores of
+ * the exact 8-bit K, as the reference's quantised kernel does
+ * (flashattn_tile/kernels/decode.py:419-429), fp8 V is round_to_fp16(
+ * float(x) * scale) and int8 V is x * fp16(scale), within one fp16 ulp of
+ * it; the results stay within the dequantise-then-attend tolerance.
  */
 typedef struct fat_decode_args {
   const void* q;
