@@ -12,8 +12,10 @@ Drop-in for ``flashattn_tile/quant.py`` (same names and semantics):
 On ROCm tensors the quantisation itself is the HIP kernel ``fat_quantize_pages``
 (one pass over the pages, bit-exact to the formulas above); CPU tensors take
 the torch expressions.  The HIP decode kernels apply the dequantisation in
-registers, so a quantised cache costs 1 byte per element of HBM traffic plus
-8 bytes of scales per (page, KV head).  On gfx950 float8_e4m3fn is the OCP encoding the hardware
+registers (with fp16 queries: K staged as its exact 8-bit values and k_scale
+applied to the fp32 scores, as the reference's quantised kernel does,
+``kernels/decode.py:419-429``), so a quantised cache costs 1 byte per element
+of HBM traffic plus 8 bytes of scales per (page, KV head).  On gfx950 float8_e4m3fn is the OCP encoding the hardware
 converts natively (v_cvt_pk_f32_fp8), which is why it is the default format
 whenever a ROCm device is present.
 """
