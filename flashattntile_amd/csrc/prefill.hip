@@ -1029,8 +1029,11 @@ void prefill_pp_kernel(const PrefillParams p) {
     softmax(0);
     // Causal: tiles past this wave's last visible key are fully masked for
     // it; from tile nv on the wave only stages tiles and keeps the barrier
-    // count (two per tile) of the rest of the workgroup.
-    const int nv = CAUSAL ? min(n_tiles, (row0 + 31 + shift) / kBN + 1) : n_tiles;
+    // count (two per tile) of the rest of the workgroup.  A wave whose rows
+    // all lie past the sequence's last query (the last block of a sequence
+    // whose length is not a multiple of 256) stops after tile 0: nothing it
+    // computes is stored.
+    const int nv = row0 >= q_len ? 1 : CAUSAL ? min(n_tiles, (row0 + 31 + shift) / kBN + 1) : n_tiles;
     for (int t = 1; t < nv; ++t) {
       // sched_barrier keeps every instruction inside its phase (the compiler
       // would otherwise move MFMAs across the workgroup barrier); the MFMA
