@@ -132,6 +132,22 @@ def test_quant_decode_matches_dequantized_oracle(mode, qdtype, d, h, hk, split_k
     assert_parity(out, ref, label=label)
 
 
+@pytest.mark.parametrize("d,P", [(128, 8), (128, 32), (128, 64), (64, 16), (64, 128)])
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+def test_quant_decode_page_sizes(mode, qdtype, d, P, decode_kernel):
+    """8-bit caches at page sizes from the floor (the rows of one 16-byte
+    load, 8 at D128 and 16 at D64) up: k_scale and v_scale are applied per
+    load, whose rows must lie in one page."""
+    label = f"quant {decode_kernel} {mode} {qdtype} D{d} P{P}"
+    print(label, flush=True)
+    q, cache, scales, ref = _quant_case(ODD_LENS, 32, 8, d, P, qdtype, mode, seed=17 + P)
+    for split_k in (1, 3):
+        out = paged_decode_attention_fp8(q, cache, scales, config={"split_k": split_k})
+        torch.cuda.synchronize()
+        assert_parity(out, ref, label=f"{label} sk{split_k}")
+
+
 @pytest.mark.parametrize("order", ["random", "growing"])
 @pytest.mark.parametrize("split_k", [1, 4])
 @pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
