@@ -43,8 +43,9 @@ namespace fat {
 
 enum KvKind { KV_SAME = 0, KV_I8 = 1, KV_FP8 = 2 };
 
-// Lazy rescale bound of the MFMA decode (log2 units): m only moves when a
-// block's max exceeds it by more than this; p then stays below 2^kDecLazy.
+// Lazy rescale bound of both decode kernels (log2 units): m only moves when
+// a block's or unit's max exceeds it by more than this; p then stays below
+// 2^kDecLazy.
 constexpr float kDecLazy = 8.0f;
 
 // fp16/bf16 K/V with at least this many query heads per KV head use the MFMA
@@ -319,8 +320,13 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
       }
       mx = within_quad<OpMax, LPH>(mx);
       mx = across_rows<OpMax, LPR>(mx);
-      const float m_new = fmaxf(m_run[hh], mx);
-      alpha[hh] = fast_exp2(m_run[hh] - m_new);
+      // Lazy max: m moves (and acc / l are rescaled) only when a unit's max
+      // exceeds it by more than kDecLazy, so p = 2^(s - m) stays below
+      // 2^kDecLazy -- exact in the fp32 sums and PV -- and most units skip
+      // the rescale.
+      const bool grow = mx > m_run[hh] + kDecLazy;
+      const float m_new = grow ? mx : m_run[hh];
+      alpha[hh] = grow ? fast_exp2(m_run[hh] - m_new) : 1.f;
       float ps = 0.f;
 #pragma unroll
       for (int v = 0; v < VPH; ++v) {
@@ -364,10 +370,16 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     wave_lds_fence();
 
     // ---- acc = acc * alpha + sum_i p_i * v_i (fp32) ----
+    // al[] is the same for every lane of the wave (read back from LDS).
+    bool rescale = false;
 #pragma unroll
-    for (int g = 0; g < HG; ++g)
+    for (int g = 0; g < HG; ++g) rescale |= al[g] != 1.f;
+    if (rescale) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] *= al[g];
+      for (int g = 0; g < HG; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] *= al[g];
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       float vf[EPL];
