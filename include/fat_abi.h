@@ -43,7 +43,8 @@
 extern "C" {
 #endif
 
-#define FAT_ABI_VERSION 6
+/* 7: the prefill `kernel` field accepts FAT_KERNEL_PREFILL_4WAVE_SPLIT. */
+#define FAT_ABI_VERSION 7
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
