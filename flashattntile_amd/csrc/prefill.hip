@@ -582,9 +582,6 @@ void prefill_kernel(const PrefillParams p) {
     if constexpr (VH) v_scale_offsets<CPR>(vsc[grp][buf], g, e_acc, acc, off, back);
 
     // ---- S(t+1) on the MFMA pipe, interleaved with P(t) = 2^(s c - m) ----
-#ifdef FAT_PF_PRIO
-    __builtin_amdgcn_s_setprio(1);
-#endif
     f32x16 s_nxt[2];
     if constexpr (HAS_NEXT) qk(buf ^ 1, s_nxt);
     const float cm = POS ? c : 1.f;
@@ -623,9 +620,6 @@ void prefill_kernel(const PrefillParams p) {
           acc[db] = Mfma<F16>::mma(a, pf[jb][t], acc[db]);  // fp16 V and P (bf16: scaled V)
         }
       }
-#ifdef FAT_PF_PRIO
-    __builtin_amdgcn_s_setprio(0);
-#endif
     if constexpr (HAS_NEXT) {
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) s_cur[jb] = s_nxt[jb];
