@@ -7,10 +7,17 @@
 // j <= i + kv_len - q_len) and writes q.dtype.
 //
 // MI355X design (not a translation of the Triton program):
-//   * workgroup = 4 waves x 32 query rows (BM = 128); K/V blocks of BN = 64
-//     keys are staged in LDS in their natural [key][dim] layout and shared by
-//     the 4 waves; the next block is prefetched into registers while the
-//     current one is computed;
+//   * three kernels, chosen per launch from the grid size and the longest
+//     key chain (launch_prefill): prefill_pp_kernel, 8 waves x 32 query rows
+//     (256 rows) whose two 4-wave groups run MFMA and softmax phases in
+//     ping-pong on each SIMD, for grids that cover the CUs;
+//     prefill_kernel<NG = 1>, 4 waves x 32 rows (BM = 128), for smaller
+//     grids; prefill_kernel<NG = 2>, two such groups on the same 128 rows
+//     taking alternate key tiles (merged through LDS at the end), for grids
+//     that leave CUs idle;
+//   * K/V blocks of BN = 64 keys are staged in LDS in their natural
+//     [key][dim] layout and shared by the waves; the next blocks are
+//     prefetched into registers while the current one is computed;
 //   * scores are computed transposed, S^T = K Q^T, with
 //     v_mfma_f32_32x32x16_{f16,bf16}: the accumulator then holds one query
 //     per lane (column) and 32 keys per lane pair, so the softmax row max /
@@ -21,12 +28,11 @@
 //     accumulator layout), and V^T comes from LDS through
 //     ds_read_b64_tr_b16, so V never needs a transposed copy;
 //   * P is rounded to fp16 for the PV product (prefill.py:128 rounds it to
-//     the input dtype).  For bf16 inputs the 8-wave kernel stages V as fp16,
-//     each staging wave's rows scaled by a power of two that is 1 unless
-//     some |v| >= 2^15, and folds the scales into P's exponent; the 4-wave
-//     kernel multiplies bf16 V by P split into hi + lo bf16 parts.  Both keep
-//     the result within fp32-level error of the fp32 reference (the first
-//     adds at most max|v| * 2^-39 per V element when |v| reaches 2^15);
+//     the input dtype).  For bf16 inputs both kernels stage V as fp16, each
+//     staging wave's rows scaled by a power of two that is 1 unless some
+//     |v| >= 2^15, and fold the scales into P's exponent: the result stays
+//     within fp32-level error of the fp32 reference (at most max|v| * 2^-39
+//     per V element once |v| reaches 2^15);
 //   * exp is 2^(x * log2 e) on v_exp_f32;
 //   * the 1-D grid walks query blocks longest-first (causal balance) and
 //     assigns the query heads that share a KV head to the same XCD
@@ -36,9 +42,11 @@
 //     key j of sequence b is slot j % P of page page_table[b, j / P], and
 //     kv_len is seq_lens[b].  Page ids are loaded one tile ahead, so the
 //     table lookup is off the load's critical path.  When a page holds at
-//     least the rows of one 16-byte-per-lane load (PG 2) the page id is
-//     wave-uniform and a load is a scalar base plus a constant lane offset;
-//     otherwise (PG 1) each lane forms its own 64-bit address.
+//     least the rows of one 16-byte-per-lane load (PG 2, PG 3) the page id is
+//     wave-uniform and a load is a scalar base plus a constant lane offset
+//     (PG 3: one pool descriptor and a 32-bit offset, when every row of the
+//     pool lies within 2^31 bytes); otherwise (PG 1) each lane forms its own
+//     64-bit address.
 #include <stdlib.h>
 #include <string.h>
 
