@@ -784,8 +784,12 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 
 // Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
 //   M = max_s m_s, w_s = 2^(m_s - M), o = sum_s acc_s w_s / sum_s l_s w_s.
-// Rows are (sequence, token, head) with T tokens per sequence.
-template <typename QT>
+// Rows are (sequence, token, head) with T tokens per sequence.  SMAX (a
+// power of two >= S) fixes the trip count so the loops unroll: every
+// partition's (m, l) and acc loads of a thread are issued before the first
+// is used, one memory latency per launch instead of one per partition (a
+// runtime-bounded loop issued them one at a time: 12.9 us at S = 32).
+template <typename QT, int SMAX>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ ws_acc,
                                                            const float* __restrict__ ws_ml, uint8_t* out,
                                                            int B, int T, int H, int D, int S, int64_t o_sb,
@@ -800,14 +804,34 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   const int b = bt / T;
   const float* ml = ws_ml + bh * S * 2;
   const float* acc = ws_acc + bh * S * D + d;
+  // Padded partitions (s >= S) re-read partition S - 1, so every address is
+  // inside this row, and are then given m = -inf (weight 0).
+  float m[SMAX], l[SMAX], a[SMAX];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const int sc = min(s, S - 1);
+    m[s] = ml[2 * sc];
+    l[s] = ml[2 * sc + 1];
+    a[s] = acc[(int64_t)sc * D];
+  }
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    if (s >= S) {
+      m[s] = -INFINITY;
+      l[s] = 0.f;
+      a[s] = 0.f;
+    }
+  }
   float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) M = fmaxf(M, m[s]);
   float A = 0.f, L = 0.f;
   if (M != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float f = fast_exp2(ml[2 * s] - M);
-      A = __builtin_fmaf(acc[(int64_t)s * D], f, A);
-      L = __builtin_fmaf(ml[2 * s + 1], f, L);
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const float f = fast_exp2(m[s] - M);  // 0 for padded or empty partitions
+      A = __builtin_fmaf(a[s], f, A);
+      L = __builtin_fmaf(l[s], f, L);
     }
   }
   const float o = L > 0.f ? A / L : 0.f;
@@ -883,18 +907,28 @@ void launch_decode_mfma_q(const fat::DecodeParams& prm, int kv, int D, int nw, d
   }
 }
 
+template <typename QT, int SMAX>
+void launch_merge_s(const fat::DecodeParams& prm, const fat_decode_args* a, int D, dim3 mgrid, hipStream_t stream) {
+  hipLaunchKernelGGL((fat::decode_merge_kernel<QT, SMAX>), mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
+                     prm.out, a->batch, prm.T, a->num_heads, D, a->split_k, a->out_stride_b, prm.o_st,
+                     a->out_stride_h);
+}
+
+template <typename QT>
+void launch_merge_q(const fat::DecodeParams& prm, const fat_decode_args* a, int D, dim3 mgrid, hipStream_t stream) {
+  const int S = a->split_k;
+  if (S <= 4) launch_merge_s<QT, 4>(prm, a, D, mgrid, stream);
+  else if (S <= 8) launch_merge_s<QT, 8>(prm, a, D, mgrid, stream);
+  else if (S <= 16) launch_merge_s<QT, 16>(prm, a, D, mgrid, stream);
+  else if (S <= 32) launch_merge_s<QT, 32>(prm, a, D, mgrid, stream);
+  else launch_merge_s<QT, 64>(prm, a, D, mgrid, stream);  // split_k <= 64 (validated)
+}
+
 int launch_merge(const fat::DecodeParams& prm, const fat_decode_args* a, int D, hipStream_t stream) {
   const int64_t n = (int64_t)a->batch * prm.T * a->num_heads * D;
   const dim3 mgrid((unsigned)((n + 255) / 256));
-  if (a->q_dtype == FAT_DTYPE_F16) {
-    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::F16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, prm.T, a->num_heads, D, a->split_k, a->out_stride_b, prm.o_st,
-                       a->out_stride_h);
-  } else {
-    hipLaunchKernelGGL(fat::decode_merge_kernel<fat::BF16>, mgrid, dim3(256), 0, stream, prm.ws_acc, prm.ws_ml,
-                       prm.out, a->batch, prm.T, a->num_heads, D, a->split_k, a->out_stride_b, prm.o_st,
-                       a->out_stride_h);
-  }
+  if (a->q_dtype == FAT_DTYPE_F16) launch_merge_q<fat::F16>(prm, a, D, mgrid, stream);
+  else launch_merge_q<fat::BF16>(prm, a, D, mgrid, stream);
   return fat_host::launch_status("decode_merge_kernel");
 }
 
