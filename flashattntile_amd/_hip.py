@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # enum fat_dtype
 DT_F16 = 0
@@ -33,9 +33,15 @@ DT_F32 = 4
 KERNEL_AUTO = 0
 KERNEL_DECODE_VALU = 1
 KERNEL_DECODE_MFMA = 2
+KERNEL_DECODE_GENERIC = 3
 KERNEL_PREFILL_PINGPONG = 1
 KERNEL_PREFILL_4WAVE = 2
 KERNEL_PREFILL_4WAVE_SPLIT = 3
+
+# enum fat_rows (the `rows` field of the paged prefill arguments)
+ROWS_AUTO = 0
+ROWS_WIDE = 1
+ROWS_LANE = 2
 
 EXPORTED_SYMBOLS = (
     "fat_abi_version",
@@ -169,6 +175,7 @@ class PrefillPagedArgs(ctypes.Structure):
         ("dtype", _c_i32),
         ("softmax_scale", ctypes.c_float),
         ("kernel", _c_i32),
+        ("rows", _c_i32),
     ]
 
 
@@ -493,6 +500,7 @@ def prefill_paged(
     softmax_scale: float,
     stream: int | None = None,
     kernel: int = KERNEL_AUTO,
+    rows: int = ROWS_AUTO,
 ) -> None:
     """Enqueue ``fat_prefill_paged`` for already-validated device tensors."""
     a = PrefillPagedArgs()
@@ -521,6 +529,7 @@ def prefill_paged(
     a.dtype = dtype_code(q.dtype)
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
+    a.rows = int(rows)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_prefill_paged(ctypes.byref(a), _c_vp(handle)), "fat_prefill_paged")
 

@@ -31,7 +31,6 @@ from __future__ import annotations
 import json
 import math
 import os
-import statistics
 import time
 import warnings
 from datetime import datetime, timezone
@@ -380,53 +379,58 @@ def build_config_space(kind: str, *, batch: int = 1, num_heads: int = 32, num_kv
 
 
 def time_callable(fn, warmup: int = 10, iters: int = 50, flush=None) -> list[float]:
-    """Per-iteration latencies in milliseconds (``autotune.py:207-240``).
+    """Per-call latencies of ``fn`` in milliseconds (the role of
+    ``autotune.py:241-271``).
 
-    Device work is timed with HIP events on torch's current stream, which is
-    where the kernels are enqueued.  ``flush`` (a callable, e.g. clearing a
-    512 MiB buffer) runs before every timed call, outside the events, so the
-    256 MB MALL does not serve a working set that fits in it."""
+    On a ROCm device every call is bracketed by its own pair of HIP events on
+    torch's current stream (where the kernels are enqueued); all ``iters``
+    calls are enqueued first and the events are read after one final
+    synchronisation, so no host round trip sits between two calls.
+    ``flush`` (e.g. clearing a 512 MiB buffer) is enqueued before each timed
+    call, outside its events, so the 256 MB MALL does not serve a working set
+    that fits in it.  Without a device the calls are timed on the host clock.
+    Timing inside a graph capture is refused."""
     import torch
 
     if warmup < 1 or iters < 1:
         raise ValueError("warmup and iters must be >= 1")
-    times: list[float] = []
-    if torch.cuda.is_available() and not torch.cuda.is_current_stream_capturing():
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        for _ in range(iters):
-            if flush is not None:
-                flush()
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record()
-            fn()
-            end.record()
-            end.synchronize()
-            times.append(float(start.elapsed_time(end)))
-        return times
+    on_device = torch.cuda.is_available()
+    if on_device and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("time_callable cannot time inside a graph capture")
     for _ in range(warmup):
         fn()
-    for _ in range(iters):
-        t0 = time.perf_counter()
+    if not on_device:
+        out = []
+        for _ in range(iters):
+            t0 = time.perf_counter_ns()
+            fn()
+            out.append((time.perf_counter_ns() - t0) / 1e6)
+        return out
+    torch.cuda.synchronize()
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for begin, end in marks:
+        if flush is not None:
+            flush()
+        begin.record()
         fn()
-        times.append((time.perf_counter() - t0) * 1000.0)
-    return times
+        end.record()
+    torch.cuda.synchronize()
+    return [float(begin.elapsed_time(end)) for begin, end in marks]
 
 
 def summarize_times(times: list[float]) -> dict:
-    """median / mean / min / p90 of :func:`time_callable` output (``autotune.py:243-254``)."""
-    if not times:
+    """``median_ms`` / ``mean_ms`` / ``min_ms`` / ``p90_ms`` (nearest-rank
+    90th percentile) and ``iters`` of a list of latencies (the columns of
+    ``autotune.py:274-287``)."""
+    vals = sorted(float(t) for t in times)
+    n = len(vals)
+    if n == 0:
         raise ValueError("no timings")
-    ordered = sorted(times)
-    return {
-        "median_ms": statistics.median(times),
-        "mean_ms": statistics.fmean(times),
-        "min_ms": ordered[0],
-        "p90_ms": ordered[min(len(ordered) - 1, int(math.ceil(0.9 * len(ordered))) - 1)],
-        "iters": len(times),
-    }
+    half = n // 2
+    median = vals[half] if n % 2 else 0.5 * (vals[half - 1] + vals[half])
+    rank90 = -(-9 * n // 10)  # smallest rank r with r / n >= 0.9
+    return {"median_ms": median, "mean_ms": math.fsum(vals) / n, "min_ms": vals[0], "p90_ms": vals[rank90 - 1],
+            "iters": n}
 
 
 def time_back_to_back(fn, warmup: int = 3, reps: int = 5, per_rep: int = 20) -> list[float]:

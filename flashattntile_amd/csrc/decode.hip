@@ -37,11 +37,10 @@
 
 #include <type_traits>
 
-#include "fat_common.h"
+#include "decode_params.h"
 
 namespace fat {
 
-enum KvKind { KV_SAME = 0, KV_I8 = 1, KV_FP8 = 2 };
 
 // Lazy rescale bound of both decode kernels (log2 units): m only moves when
 // a block's or unit's max exceeds it by more than this; p then stays below
@@ -49,35 +48,12 @@ enum KvKind { KV_SAME = 0, KV_I8 = 1, KV_FP8 = 2 };
 constexpr float kDecLazy = 8.0f;
 
 // fp16/bf16 K/V with at least this many query heads per KV head use the MFMA
-// decode (FAT_DECODE_KERNEL=valu|mfma overrides the choice).
+// decode (the `kernel` argument field overrides the choice).
 constexpr int kDecMfmaMinGroup = 8;
 #ifndef FAT_DEC_MFMA_8BIT
 #define FAT_DEC_MFMA_8BIT 1
 #endif
 
-struct DecodeParams {
-  const uint8_t* q;
-  const uint8_t* k;
-  const uint8_t* v;
-  const float* ks;
-  const float* vs;
-  const int32_t* pt;
-  const int32_t* lens;
-  uint8_t* out;
-  float* ws_acc;  // [B, H, S, D]
-  float* ws_ml;   // [B, H, S, 2]  (m in log2 units, l)
-  int64_t q_sb, q_sh, q_st;
-  int64_t k_sp, k_ss, k_sh;
-  int64_t v_sp, v_ss, v_sh;
-  int64_t sc_sp, sc_sh;
-  int64_t pt_sb;
-  int64_t o_sb, o_sh, o_st;
-  int32_t H, Hkv, group, hg_per_kv;
-  int32_t T;  // query tokens per sequence (1 = single-query decode)
-  int32_t P, log2P, num_pages, max_pages;
-  int32_t pps_fixed;  // pages per partition, 0 = ceil(np / split_k)
-  float scale_log2;  // softmax_scale * log2(e)
-};
 
 // Lane geometry for one 16-byte load per lane.
 template <int KV, int D>
@@ -834,9 +810,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
       L = __builtin_fmaf(l[s], f, L);
     }
   }
-  const float o = L > 0.f ? A / L : 0.f;
-  uint16_t* op = reinterpret_cast<uint16_t*>(out) + (b * o_sb + t * o_st + h * o_sh + d);
-  *op = Pair<QT>::from_float(o);
+  store_elem<QT>(out, (int64_t)b * o_sb + (int64_t)t * o_st + (int64_t)h * o_sh + d, L > 0.f ? A / L : 0.f);
 }
 
 }  // namespace fat
@@ -863,14 +837,18 @@ int launch_decode_t(const fat::DecodeParams& prm, int nw, dim3 grid, hipStream_t
   return fat_host::launch_status("paged_decode_kernel");
 }
 
+// 8-bit caches take the VALU kernel only with 4-head groups: the 8-head
+// instantiations with in-register dequantisation spill (the MFMA kernel is
+// the library's choice for 8-bit caches anyway).
 template <typename QT, int KV>
 int launch_decode_kv(const fat::DecodeParams& prm, int D, int HG, int nw, dim3 grid, hipStream_t stream) {
-  if (D == 128) {
-    return HG == 8 ? launch_decode_t<QT, KV, 128, 8>(prm, nw, grid, stream)
-                   : launch_decode_t<QT, KV, 128, 4>(prm, nw, grid, stream);
+  if constexpr (KV == fat::KV_SAME) {
+    if (HG == 8)
+      return D == 128 ? launch_decode_t<QT, KV, 128, 8>(prm, nw, grid, stream)
+                      : launch_decode_t<QT, KV, 64, 8>(prm, nw, grid, stream);
   }
-  return HG == 8 ? launch_decode_t<QT, KV, 64, 8>(prm, nw, grid, stream)
-                 : launch_decode_t<QT, KV, 64, 4>(prm, nw, grid, stream);
+  return D == 128 ? launch_decode_t<QT, KV, 128, 4>(prm, nw, grid, stream)
+                  : launch_decode_t<QT, KV, 64, 4>(prm, nw, grid, stream);
 }
 
 template <typename QT>
@@ -928,7 +906,8 @@ int launch_merge(const fat::DecodeParams& prm, const fat_decode_args* a, int D, 
   const int64_t n = (int64_t)a->batch * prm.T * a->num_heads * D;
   const dim3 mgrid((unsigned)((n + 255) / 256));
   if (a->q_dtype == FAT_DTYPE_F16) launch_merge_q<fat::F16>(prm, a, D, mgrid, stream);
-  else launch_merge_q<fat::BF16>(prm, a, D, mgrid, stream);
+  else if (a->q_dtype == FAT_DTYPE_BF16) launch_merge_q<fat::BF16>(prm, a, D, mgrid, stream);
+  else launch_merge_q<fat::F32>(prm, a, D, mgrid, stream);
   return fat_host::launch_status("decode_merge_kernel");
 }
 
@@ -963,16 +942,16 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     fat_host::set_error("fat_paged_decode: split_k must be in [1, 64], got %d", a->split_k);
     return FAT_E_INVALID;
   }
-  if (a->q_dtype != FAT_DTYPE_F16 && a->q_dtype != FAT_DTYPE_BF16) {
-    fat_host::set_error("fat_paged_decode: q_dtype must be fp16 or bf16");
+  if (a->q_dtype != FAT_DTYPE_F16 && a->q_dtype != FAT_DTYPE_BF16 && a->q_dtype != FAT_DTYPE_F32) {
+    fat_host::set_error("fat_paged_decode: q_dtype must be fp16, bf16 or fp32");
     return FAT_E_UNSUPPORTED;
   }
   int kv;
   if (a->kv_dtype == a->q_dtype) kv = fat::KV_SAME;
-  else if (a->kv_dtype == FAT_DTYPE_I8) kv = fat::KV_I8;
-  else if (a->kv_dtype == FAT_DTYPE_FP8E4M3) kv = fat::KV_FP8;
+  else if (a->q_dtype != FAT_DTYPE_F32 && a->kv_dtype == FAT_DTYPE_I8) kv = fat::KV_I8;
+  else if (a->q_dtype != FAT_DTYPE_F32 && a->kv_dtype == FAT_DTYPE_FP8E4M3) kv = fat::KV_FP8;
   else {
-    fat_host::set_error("fat_paged_decode: kv_dtype must equal q_dtype or be int8/fp8e4m3");
+    fat_host::set_error("fat_paged_decode: kv_dtype must equal q_dtype, or be int8/fp8e4m3 with fp16/bf16 queries");
     return FAT_E_UNSUPPORTED;
   }
   if (kv != fat::KV_SAME && (!a->k_scale || !a->v_scale)) {
@@ -980,17 +959,15 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 64 && D != 128) {
-    fat_host::set_error("fat_paged_decode: head_dim %d unsupported (64 or 128)", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    fat_host::set_error("fat_paged_decode: head_dim %d unsupported (32, 64, 128 or 256)", D);
     return FAT_E_UNSUPPORTED;
+  }
+  if (a->page_size < 1) {
+    fat_host::set_error("fat_paged_decode: page_size must be positive, got %d", a->page_size);
+    return FAT_E_INVALID;
   }
   const int log2P = ilog2_exact(a->page_size);
-  const int rpl = (kv == fat::KV_SAME) ? (D == 128 ? 4 : 8) : (D == 128 ? 8 : 16);
-  if (log2P < 0 || a->page_size < rpl) {
-    fat_host::set_error("fat_paged_decode: page_size %d unsupported (power of two >= %d for this head_dim/dtype)",
-                        a->page_size, rpl);
-    return FAT_E_UNSUPPORTED;
-  }
   if (a->waves_per_group != 0 && a->waves_per_group != 4 && a->waves_per_group != 8) {
     fat_host::set_error("fat_paged_decode: waves_per_group must be 0 (auto), 4 or 8, got %d", a->waves_per_group);
     return FAT_E_INVALID;
@@ -1009,20 +986,41 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     return FAT_E_INVALID;
   }
   const int T = a->q_len > 1 ? a->q_len : 1;
-  if (a->kernel != FAT_KERNEL_AUTO && a->kernel != FAT_KERNEL_DECODE_VALU && a->kernel != FAT_KERNEL_DECODE_MFMA) {
-    fat_host::set_error("fat_paged_decode: kernel must be FAT_KERNEL_AUTO (0), _DECODE_VALU (1) or _DECODE_MFMA (2), "
-                        "got %d", a->kernel);
+  if (a->kernel != FAT_KERNEL_AUTO && a->kernel != FAT_KERNEL_DECODE_VALU && a->kernel != FAT_KERNEL_DECODE_MFMA &&
+      a->kernel != FAT_KERNEL_DECODE_GENERIC) {
+    fat_host::set_error("fat_paged_decode: kernel must be FAT_KERNEL_AUTO (0), _DECODE_VALU (1), _DECODE_MFMA (2) "
+                        "or _DECODE_GENERIC (3), got %d", a->kernel);
     return FAT_E_INVALID;
   }
   if (a->kernel == FAT_KERNEL_DECODE_VALU && T > 1) {
     fat_host::set_error("fat_paged_decode: the VALU decode kernel takes one query per sequence (q_len %d)", T);
     return FAT_E_UNSUPPORTED;
   }
-  // 16-byte alignment of every row start the kernel loads.
-  const int eb = (kv == fat::KV_SAME) ? 2 : 1;
-  const uintptr_t align_or = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
-                             (uintptr_t)(2 * a->q_stride_b) | (uintptr_t)(2 * a->q_stride_h) |
-                             (uintptr_t)(T > 1 ? 2 * a->q_stride_t : 0) |
+  // The VALU and MFMA kernels take fp16/bf16 queries, head_dim 64 or 128 and
+  // power-of-two pages of at least the rows one 16-byte load per lane covers
+  // (their loads read one page id per load); the generic kernel takes the rest.
+  const int rpl = (kv == fat::KV_SAME) ? (D == 128 ? 4 : 8) : (D == 128 ? 8 : 16);
+  const bool fast_ok = a->q_dtype != FAT_DTYPE_F32 && (D == 64 || D == 128) && log2P >= 0 && a->page_size >= rpl;
+  const bool generic = a->kernel == FAT_KERNEL_DECODE_GENERIC || (a->kernel == FAT_KERNEL_AUTO && !fast_ok);
+  if (!generic && !fast_ok) {
+    fat_host::set_error("fat_paged_decode: the %s decode kernel takes fp16/bf16 queries, head_dim 64 or 128 and "
+                        "power-of-two pages of at least %d rows (page_size %d, head_dim %d); use "
+                        "FAT_KERNEL_AUTO or FAT_KERNEL_DECODE_GENERIC", a->kernel == FAT_KERNEL_DECODE_VALU ? "VALU"
+                        : "MFMA", rpl, a->page_size, D);
+    return FAT_E_UNSUPPORTED;
+  }
+  if (generic && T > 1) {
+    fat_host::set_error("fat_paged_decode: multi-token decode (q_len %d) runs on the MFMA kernel, which takes "
+                        "fp16/bf16, head_dim 64 or 128 and power-of-two pages of at least %d rows", T, rpl);
+    return FAT_E_UNSUPPORTED;
+  }
+  // 16-byte alignment of every row start the kernels load.
+  const int qeb = a->q_dtype == FAT_DTYPE_F32 ? 4 : 2;
+  const int eb = (kv == fat::KV_SAME) ? qeb : 1;
+  const uintptr_t q_align = generic ? 0
+                                    : ((uintptr_t)a->q | (uintptr_t)(qeb * a->q_stride_b) |
+                                       (uintptr_t)(qeb * a->q_stride_h) | (uintptr_t)(T > 1 ? qeb * a->q_stride_t : 0));
+  const uintptr_t align_or = q_align | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
                              (uintptr_t)(eb * a->k_stride_page) | (uintptr_t)(eb * a->k_stride_slot) |
                              (uintptr_t)(eb * a->k_stride_head) | (uintptr_t)(eb * a->v_stride_page) |
                              (uintptr_t)(eb * a->v_stride_slot) | (uintptr_t)(eb * a->v_stride_head);
@@ -1033,14 +1031,16 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
 
   const int group = a->num_heads / a->num_kv_heads;
   bool use_mfma = group >= fat::kDecMfmaMinGroup || (kv != fat::KV_SAME && FAT_DEC_MFMA_8BIT);
-  if (a->kernel != FAT_KERNEL_AUTO) {
+  if (a->kernel == FAT_KERNEL_DECODE_VALU || a->kernel == FAT_KERNEL_DECODE_MFMA)
     use_mfma = a->kernel == FAT_KERNEL_DECODE_MFMA;
-  } else if (const char* force = getenv("FAT_DECODE_KERNEL")) {
-    if (!strcmp(force, "mfma")) use_mfma = true;
-    else if (!strcmp(force, "valu")) use_mfma = false;
-  }
   if (T > 1) use_mfma = true;  // only the MFMA kernel has per-token rows
-  const int HG = use_mfma ? 32 : (group >= 8 ? 8 : 4);
+  if (!generic && !use_mfma && kv != fat::KV_SAME && group >= 8) {
+    fat_host::set_error("fat_paged_decode: the VALU decode takes int8/fp8 caches for GQA groups below 8 "
+                        "(group %d); use FAT_KERNEL_AUTO or FAT_KERNEL_DECODE_MFMA", group);
+    return FAT_E_UNSUPPORTED;
+  }
+  const int HG = generic ? (group < fat_host::kGenericHeads ? group : fat_host::kGenericHeads)
+                         : (use_mfma ? 32 : (group >= 8 ? 8 : 4));
   const int hg_per_kv = (group * T + HG - 1) / HG;
 
   fat::DecodeParams prm{};
@@ -1087,13 +1087,17 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   const int64_t wgs = (int64_t)grid.x * grid.y * grid.z;
   const int64_t pages_per_wg =
       a->pages_per_split > 0 ? a->pages_per_split : ((int64_t)a->max_pages + a->split_k - 1) / a->split_k;
+  if (generic) {
+    const int rc = fat_host::launch_decode_generic(prm, a->q_dtype, kv, D, HG, grid, stream);
+    if (rc != FAT_OK || a->split_k == 1) return rc;
+    return launch_merge(prm, a, D, stream);
+  }
   if (use_mfma) {
     // 8 waves per workgroup pay off only when the grid leaves CUs short of
     // workgroups and each partition is long (>= 2048 keys, measured on
     // MI355X); short partitions finish sooner with 4.
     int nw = a->waves_per_group ? a->waves_per_group
                                 : ((wgs < 2 * 256 && pages_per_wg * a->page_size >= 2048) ? 8 : 4);
-    if (const char* force = getenv("FAT_DECODE_MFMA_WAVES")) nw = atoi(force) == 8 ? 8 : 4;
     if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, nw, grid, stream);
     else launch_decode_mfma_q<fat::BF16>(prm, kv, D, nw, grid, stream);
     const int rc = fat_host::launch_status("paged_decode_mfma_kernel");

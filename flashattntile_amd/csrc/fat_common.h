@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/fat_abi.h"
 
 namespace fat {
@@ -37,6 +39,15 @@ __device__ __forceinline__ u32 as_u32(float x) { return __builtin_bit_cast(u32, 
 // Element types as template tags.
 struct F16 {};
 struct BF16 {};
+struct F32 {};
+
+// Element bytes and the final store of one output element of type T.
+template <typename T> struct Elem {
+  static constexpr int kBytes = 2;
+};
+template <> struct Elem<F32> {
+  static constexpr int kBytes = 4;
+};
 
 template <typename T> struct Pair;
 template <> struct Pair<F16> {
@@ -69,6 +80,17 @@ template <> struct Pair<BF16> {
     return __builtin_bit_cast(uint16_t, (bf16)x);
   }
 };
+
+// Store x as element `idx` of an output array of element type T (16-bit
+// types round to nearest even).
+template <typename T>
+__device__ __forceinline__ void store_elem(uint8_t* base, int64_t idx, float x) {
+  if constexpr (std::is_same<T, F32>::value) {
+    reinterpret_cast<float*>(base)[idx] = x;
+  } else {
+    reinterpret_cast<uint16_t*>(base)[idx] = Pair<T>::from_float(x);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // 8-bit KV storage decoding.  Each returns four floats from one dword.

@@ -31,8 +31,6 @@
 
 namespace fat {
 
-struct F32 {};
-
 template <typename S> struct SrcBytes { static constexpr int kValue = 2; };
 template <> struct SrcBytes<F32> { static constexpr int kValue = 4; };
 

@@ -1147,9 +1147,8 @@ bool valid_prefill_kernel(int kernel) {
 // FAT_PF_SPLIT_MAX workgroups) and the chain is at least FAT_PF_SPLIT_TILES
 // tiles, or, causal, when it has at most 2 FAT_PF_SPLIT_MAX workgroups and
 // chains of at least FAT_PF_SPLIT_LONG tiles (the merge then costs less than
-// the balance gained).  A non-AUTO `kernel` argument forces one kernel; with
-// AUTO, FAT_PREFILL_KERNEL=pingpong|4wave|4wave_split overrides the choice (tests
-// exercise every kernel on every shape).
+// the balance gained).  A non-AUTO `kernel` argument forces one kernel (the
+// tests run every kernel on every shape that way).
 template <int PG>
 int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
                    float softmax_scale, int kernel, const char* who, hipStream_t stream) {
@@ -1166,10 +1165,6 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     kind = kernel == FAT_KERNEL_PREFILL_PINGPONG ? PF_PINGPONG
            : kernel == FAT_KERNEL_PREFILL_4WAVE  ? PF_4WAVE
                                                  : PF_4WAVE_SPLIT;
-  } else if (const char* force = getenv("FAT_PREFILL_KERNEL")) {
-    if (!strcmp(force, "pingpong")) kind = PF_PINGPONG;
-    else if (!strcmp(force, "4wave")) kind = PF_4WAVE;
-    else if (!strcmp(force, "4wave_split")) kind = PF_4WAVE_SPLIT;
   }
   const int bm = kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
   prm.nqb = (max_seqlen_q + bm - 1) / bm;
@@ -1323,6 +1318,10 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     fat_host::set_error("fat_prefill_paged: max_seqlen_q must be non-negative");
     return FAT_E_INVALID;
   }
+  if (a->rows != FAT_ROWS_AUTO && a->rows != FAT_ROWS_WIDE && a->rows != FAT_ROWS_LANE) {
+    fat_host::set_error("fat_prefill_paged: rows must be FAT_ROWS_AUTO (0), _WIDE (1) or _LANE (2), got %d", a->rows);
+    return FAT_E_INVALID;
+  }
   const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
                             (uintptr_t)(2 * a->q_stride_t) | (uintptr_t)(2 * a->q_stride_h) |
                             (uintptr_t)(2 * a->k_stride_page) | (uintptr_t)(2 * a->k_stride_slot) |
@@ -1372,12 +1371,10 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   const int64_t vspan =
       (int64_t)(a->num_pages - 1) * 2 * a->v_stride_page + (int64_t)(P - 1) * 2 * a->v_stride_slot + 2 * D;
   bool off32 = kspan < 0x7fffffffLL && vspan < 0x7fffffffLL;
-  // FAT_PREFILL_PAGED_ROWS=lane forces the per-lane variant, =wide the
-  // uniform one with 64-bit row addresses (tests).
-  if (const char* force = getenv("FAT_PREFILL_PAGED_ROWS")) {
-    if (!strcmp(force, "lane")) uniform = false;
-    else if (!strcmp(force, "wide")) off32 = false;
-  }
+  // `rows` forces the per-lane variant (FAT_ROWS_LANE) or the uniform one
+  // with 64-bit row addresses (FAT_ROWS_WIDE); all three give identical bits.
+  if (a->rows == FAT_ROWS_LANE) uniform = false;
+  else if (a->rows == FAT_ROWS_WIDE) off32 = false;
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const int64_t kv_bound = (int64_t)a->max_pages * P;  // longest context the table can hold
   if (uniform && off32)

@@ -1,15 +1,16 @@
-"""MI355X spec peaks and a small device probe.
+"""MI355X spec peaks and the host/device facts a measurement records.
 
 Replaces the NVIDIA tables of ``flashattn_tile/env.py:31-56``: the roofline
-denominators here are AMD's published MI355X figures (dense, no sparsity).
+denominators here are AMD's published MI355X figures (dense, no sparsity),
+and :func:`host_info` / :func:`cpu_threads` describe the CPU the oracle
+baseline runs on (``bench.py`` takes both from here).
 """
 
 from __future__ import annotations
 
+import math
 import os
 import platform
-
-import torch
 
 MI355X = {
     "name": "AMD Instinct MI355X",
@@ -32,7 +33,25 @@ def peak_mfma_tflops(dtype: str = "fp16") -> float:
     return MI355X["mfma_dense_tflops"][dtype]
 
 
+def _cgroup_cpu_quota() -> float | None:
+    """CPUs this process may use per the cgroup v2 ``cpu.max`` quota (None
+    when unlimited or unreadable)."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            quota, period = fh.read().split()[:2]
+    except (OSError, ValueError):
+        return None
+    if quota == "max":
+        return None
+    try:
+        return float(quota) / float(period)
+    except (ValueError, ZeroDivisionError):
+        return None
+
+
 def host_info() -> dict:
+    """Affinity core count, ``os.cpu_count()``, the cgroup CPU quota and the
+    full CPU model string of this host."""
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover - non-Linux
@@ -46,10 +65,24 @@ def host_info() -> dict:
                     break
     except OSError:  # pragma: no cover
         pass
-    return {"affinity_cores": cores, "os_cpu_count": os.cpu_count(), "cpu_model": model}
+    return {"affinity_cores": cores, "os_cpu_count": os.cpu_count(), "cgroup_cpu_quota": _cgroup_cpu_quota(),
+            "cpu_model": model}
+
+
+def cpu_threads(info: dict | None = None) -> int:
+    """Threads for a CPU baseline: the affinity cores, bounded by the cgroup
+    quota when one is set (more threads than the quota only time-slice)."""
+    info = info or host_info()
+    n = info["affinity_cores"]
+    quota = info.get("cgroup_cpu_quota")
+    if quota:
+        n = min(n, max(1, math.floor(quota)))
+    return max(1, n)
 
 
 def device_info() -> dict:
+    import torch
+
     info = {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None), **host_info()}
     if torch.cuda.is_available():
         props = torch.cuda.get_device_properties(0)

@@ -55,11 +55,19 @@ __all__ = [
 # library choose from the grid size); num_stages is accepted for signature
 # compatibility with the reference's Triton knob and validated the same way,
 # but the HIP kernel's pipeline depth is fixed (one 16-token unit prefetched
-# per wave).  kernel None lets the library choose the kernel family; "valu"
-# or "mfma" forces one (what a tuning run stores for its shape).
+# per wave).  kernel None lets the library choose the kernel family; "valu",
+# "mfma" or "generic" forces one (what a tuning run stores for its shape; the
+# generic kernel is the library's own choice only for the shapes the other
+# two do not take: fp32, page sizes below their floor or not a power of two,
+# head_dim 32 or 256).
 DEFAULT_CONFIG = {"split_k": None, "num_warps": None, "num_stages": 2, "pages_per_split": None, "kernel": None}
 
-_KERNEL_CODES = {None: _hip.KERNEL_AUTO, "valu": _hip.KERNEL_DECODE_VALU, "mfma": _hip.KERNEL_DECODE_MFMA}
+_KERNEL_CODES = {None: _hip.KERNEL_AUTO, "valu": _hip.KERNEL_DECODE_VALU, "mfma": _hip.KERNEL_DECODE_MFMA,
+                 "generic": _hip.KERNEL_DECODE_GENERIC}
+
+# Element types the HIP decode kernels take for q (and for a cache of the same
+# type); int8 / float8_e4m3fn caches take fp16 / bf16 queries.
+_DECODE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 _QUANT_DTYPES = tuple(d for d in (torch.int8, getattr(torch, "float8_e4m3fn", None)) if d is not None)
 
@@ -129,9 +137,13 @@ def _merge_config(config: dict, q: torch.Tensor, cache: PagedKVCache, max_len: i
     if resolved["num_stages"] < 1:
         raise ValueError(f"num_stages must be >= 1, got {resolved['num_stages']}")
     if resolved["kernel"] not in _KERNEL_CODES:
-        raise ValueError(f"kernel must be None, 'valu' or 'mfma', got {resolved['kernel']!r}")
-    if resolved["kernel"] == "valu" and q_len > 1:
-        raise ValueError("kernel 'valu' takes one query per sequence; multi-token decode runs on 'mfma'")
+        raise ValueError(f"kernel must be None, 'valu', 'mfma' or 'generic', got {resolved['kernel']!r}")
+    if resolved["kernel"] in ("valu", "generic") and q_len > 1:
+        raise ValueError(f"kernel {resolved['kernel']!r} takes one query per sequence; multi-token decode runs "
+                         "on 'mfma'")
+    if (resolved["kernel"] == "valu" and cache.k_cache.dtype in _QUANT_DTYPES
+            and q.shape[-2] // cache.num_kv_heads >= 8):
+        raise ValueError("kernel 'valu' takes int8/float8 caches only for GQA groups below 8; use 'mfma'")
     return resolved
 
 
@@ -211,6 +223,10 @@ def paged_decode_launch(
         raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
     if out is None:
         out = torch.empty_like(q)
+    # The kernels read page_table rows with a unit column stride and seq_lens
+    # densely (the reference honours any strides, kernels/decode.py:89).
+    pt = cache.page_table if cache.page_table.stride(-1) == 1 else cache.page_table.contiguous()
+    sl = cache.seq_lens if cache.seq_lens.is_contiguous() else cache.seq_lens.contiguous()
     rows = q.shape[0] * (q.shape[1] if q.dim() == 4 else 1)
     need = _hip.decode_workspace_bytes(rows, q.shape[-2], q.shape[-1], split_k)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
@@ -219,7 +235,7 @@ def paged_decode_launch(
     if scales is not None:
         k_scale = scales["k"] if isinstance(scales, dict) else scales.k
         v_scale = scales["v"] if isinstance(scales, dict) else scales.v
-    _hip.paged_decode(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, out,
+    _hip.paged_decode(q, cache.k_cache, cache.v_cache, pt, sl, out,
                       cache.page_size, softmax_scale, split_k, workspace=workspace,
                       k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0,
                       pages_per_split=pages_per_split, kernel=_KERNEL_CODES[kernel])
@@ -235,8 +251,9 @@ def paged_decode_attention(
 ) -> torch.Tensor:
     """Paged decode attention, one query per sequence (``decode.py:533-642``).
 
-    ``q``: ``[batch, num_heads, head_dim]`` fp16/bf16 on a ROCm device; the
-    cache holds the same dtype.  ``softmax_scale`` defaults to
+    ``q``: ``[batch, num_heads, head_dim]`` fp16/bf16/fp32 on a ROCm device;
+    the cache holds the same dtype (fp32 runs on the HIP kernel too, where the
+    reference falls back to its fp32 oracle, ``decode.py:569-576``).  ``softmax_scale`` defaults to
     ``head_dim ** -0.5``.  ``config``: ``split_k`` (1 = no split; default from
     the MI355X heuristic), ``num_warps``, ``num_stages``.  ``grouped`` is
     accepted for compatibility: the HIP kernel always reads each K/V page
@@ -248,8 +265,8 @@ def paged_decode_attention(
     scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
     cfg = _resolve_config(config, q, cache, max_len, total_pages)
     _require_rocm(q, cache, "paged_decode_attention")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"paged_decode_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    if q.dtype not in _DECODE_DTYPES:
+        raise ValueError(f"paged_decode_attention: dtype {q.dtype} is not fp16/bf16/fp32 (the HIP kernels' types)")
     if cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
     return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"],
@@ -366,9 +383,10 @@ class DecodeLaunch:
         q_len = int(q.shape[1]) if multi else 1
         cfg = _resolve_config(config, q, cache, max_len, total_pages, q_len=q_len)
         _require_rocm(q, cache, "DecodeLaunch")
-        if q.dtype not in (torch.float16, torch.bfloat16):
-            raise ValueError(f"DecodeLaunch: dtype {q.dtype} is not fp16/bf16")
         quantized = cache.k_cache.dtype in _QUANT_DTYPES
+        if q.dtype not in (_DECODE_DTYPES[:2] if quantized else _DECODE_DTYPES):
+            raise ValueError(f"DecodeLaunch: q dtype {q.dtype} is not one the HIP decode takes for a "
+                             f"{cache.k_cache.dtype} cache")
         if quantized != (scales is not None):
             raise ValueError("an int8/float8 cache needs scales, and only such a cache takes them")
         if not quantized and cache.k_cache.dtype != q.dtype:
@@ -386,6 +404,10 @@ class DecodeLaunch:
                 raise ValueError("scales must be float32")
         if cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
             raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
+        # The argument block points at the engine's own table and lengths,
+        # which it updates in place: they cannot be copied to a dense layout.
+        if cache.page_table.stride(-1) != 1 or not cache.seq_lens.is_contiguous():
+            raise ValueError("DecodeLaunch: page_table rows and seq_lens must be contiguous")
         self.config = cfg
         self.softmax_scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
         rows = q.shape[0] * q_len

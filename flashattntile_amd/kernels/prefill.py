@@ -27,7 +27,7 @@ from .. import _hip
 from ..autotune import best_config, prefill_paged_signature, prefill_signature
 from ..paging import PagedKVCache, _check_layout
 
-__all__ = ["DEFAULT_CONFIG", "prefill_attention", "prefill_launch", "paged_prefill_attention",
+__all__ = ["DEFAULT_CONFIG", "PAGED_CONFIG", "prefill_attention", "prefill_launch", "paged_prefill_attention",
            "paged_prefill_launch"]
 
 DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3, "kernel": None}
@@ -35,20 +35,29 @@ DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3,
 _KERNEL_CODES = {None: _hip.KERNEL_AUTO, "pingpong": _hip.KERNEL_PREFILL_PINGPONG,
                  "4wave": _hip.KERNEL_PREFILL_4WAVE, "4wave_split": _hip.KERNEL_PREFILL_4WAVE_SPLIT}
 
+# Paged prefill's one extra knob: how K/V rows are addressed (None = the
+# fastest form the page size allows; "wide" = wave-uniform page ids with
+# 64-bit row addresses; "lane" = per-lane page ids).  All give identical bits.
+PAGED_CONFIG = {**DEFAULT_CONFIG, "rows": None}
+_ROWS_CODES = {None: _hip.ROWS_AUTO, "wide": _hip.ROWS_WIDE, "lane": _hip.ROWS_LANE}
 
-def _resolve_config(config: dict | None, kind: str | None = None, signature: str | None = None) -> dict:
+
+def _resolve_config(config: dict | None, kind: str | None = None, signature: str | None = None,
+                    defaults: dict = DEFAULT_CONFIG) -> dict:
     """``prefill.py:167-191``: an explicit config, else the stored winner for
     ``kind:signature`` (when given), else the defaults."""
-    resolved = dict(DEFAULT_CONFIG)
+    resolved = dict(defaults)
     if config is None:
         stored = best_config(kind, signature) if kind and signature else None
         if stored and stored.get("kernel", None) in _KERNEL_CODES:
             resolved["kernel"] = stored.get("kernel")
     else:
-        unknown = set(config) - set(DEFAULT_CONFIG)
+        unknown = set(config) - set(defaults)
         if unknown:
             raise ValueError(f"unknown prefill config keys: {sorted(unknown)}")
         resolved.update(config)
+    if resolved.get("rows") not in _ROWS_CODES:
+        raise ValueError(f"rows must be None, 'wide' or 'lane', got {resolved['rows']!r}")
     if resolved["kernel"] not in _KERNEL_CODES:
         raise ValueError(f"kernel must be None, 'pingpong', '4wave' or '4wave_split', got {resolved['kernel']!r}")
     for key in ("BLOCK_M", "BLOCK_N"):
@@ -142,6 +151,9 @@ def prefill_launch(
     need = _hip.prefill_workspace_bytes(k.shape[0], k.shape[1], k.shape[2])
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    # The kernels read cu_seqlens densely.
+    cu_seqlens_q = cu_seqlens_q if cu_seqlens_q.is_contiguous() else cu_seqlens_q.contiguous()
+    cu_seqlens_k = cu_seqlens_k if cu_seqlens_k.is_contiguous() else cu_seqlens_k.contiguous()
     _hip.prefill_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k,
                         causal, softmax_scale, workspace=workspace, kernel=_KERNEL_CODES[kernel])
     return out
@@ -255,17 +267,20 @@ def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
 
 def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: torch.Tensor, max_seqlen_q: int,
                          causal: bool, softmax_scale: float, out: torch.Tensor | None = None,
-                         kernel: str | None = None) -> torch.Tensor:
+                         kernel: str | None = None, rows: str | None = None) -> torch.Tensor:
     """Enqueue ``fat_prefill_paged`` without validation or synchronisation
-    (``kernel`` as for :func:`prefill_launch`)."""
+    (``kernel`` as for :func:`prefill_launch`; ``rows``: None, ``"wide"`` or
+    ``"lane"``, the row addressing of ``PAGED_CONFIG``)."""
     if q.stride(-1) != 1 or cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
         raise ValueError("q and the cache need a contiguous head_dim axis")
     if out is None:
         out = torch.empty_like(q)
     pt = cache.page_table if cache.page_table.stride(-1) == 1 else cache.page_table.contiguous()
     sl = cache.seq_lens if cache.seq_lens.is_contiguous() else cache.seq_lens.contiguous()
-    _hip.prefill_paged(q, cache.k_cache, cache.v_cache, pt, sl, cu_seqlens_q, out, cache.page_size,
-                       int(max_seqlen_q), bool(causal), float(softmax_scale), kernel=_KERNEL_CODES[kernel])
+    cu = cu_seqlens_q if cu_seqlens_q.is_contiguous() else cu_seqlens_q.contiguous()
+    _hip.prefill_paged(q, cache.k_cache, cache.v_cache, pt, sl, cu, out, cache.page_size,
+                       int(max_seqlen_q), bool(causal), float(softmax_scale), kernel=_KERNEL_CODES[kernel],
+                       rows=_ROWS_CODES[rows])
     return out
 
 
@@ -284,8 +299,8 @@ def paged_prefill_attention(
     own K/V).  Causal masking is bottom-right aligned, as in
     :func:`prefill_attention`, so query i of a q_len-token chunk sees keys
     ``j <= i + seq_lens[b] - q_len``.  ``config`` as for
-    :func:`prefill_attention` (store kind ``prefill_paged``).  Returns
-    ``q``'s shape and dtype.
+    :func:`prefill_attention` plus ``rows`` (store kind ``prefill_paged``).
+    Returns ``q``'s shape and dtype.
     """
     longest_q = _validate_paged(q, cache, cu_seqlens_q, causal)
     if max_seqlen_q <= 0:
@@ -299,8 +314,8 @@ def paged_prefill_attention(
         raise ValueError(f"paged_prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
     sig = prefill_paged_signature(cache.batch_size, q.shape[1], cache.num_kv_heads, cache.head_dim,
                                   cache.page_size, int(max_seqlen_q), causal)
-    cfg = _resolve_config(config, "prefill_paged", sig)
+    cfg = _resolve_config(config, "prefill_paged", sig, defaults=PAGED_CONFIG)
     scale = float(softmax_scale) if softmax_scale is not None else q.shape[-1] ** -0.5
     q = q if q.stride(-1) == 1 else q.contiguous()
     return paged_prefill_launch(q, cache, cu_seqlens_q, int(max_seqlen_q), bool(causal), scale,
-                                kernel=cfg["kernel"])
+                                kernel=cfg["kernel"], rows=cfg["rows"])

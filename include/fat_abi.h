@@ -43,8 +43,10 @@
 extern "C" {
 #endif
 
-/* 7: the prefill `kernel` field accepts FAT_KERNEL_PREFILL_4WAVE_SPLIT. */
-#define FAT_ABI_VERSION 7
+/* 8: fp32 decode, any page size and head_dim 32/256 through the generic
+ *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
+ *    field replaces the library's environment overrides. */
+#define FAT_ABI_VERSION 8
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -52,7 +54,8 @@ enum fat_dtype {
   FAT_DTYPE_BF16 = 1,    /* bfloat16                                       */
   FAT_DTYPE_I8 = 2,      /* symmetric int8 KV storage (scale = absmax/127) */
   FAT_DTYPE_FP8E4M3 = 3, /* OCP float8 e4m3fn KV storage (absmax/448)      */
-  FAT_DTYPE_F32 = 4      /* IEEE binary32 (fat_quantize_pages source only) */
+  FAT_DTYPE_F32 = 4      /* IEEE binary32 (decode q/K/V/out, and the
+                            fat_quantize_pages source)                     */
 };
 
 /* Kernel choice (the `kernel` field of the decode and prefill arguments).
@@ -62,11 +65,22 @@ enum fat_kernel {
   FAT_KERNEL_AUTO = 0,
   FAT_KERNEL_DECODE_VALU = 1,      /* one query per sequence (q_len <= 1)     */
   FAT_KERNEL_DECODE_MFMA = 2,      /* any cache dtype and q_len               */
+  FAT_KERNEL_DECODE_GENERIC = 3,   /* one query per sequence; every dtype,
+                                      page size and head_dim the ABI takes   */
   FAT_KERNEL_PREFILL_PINGPONG = 1, /* 8 waves, 256 query rows per workgroup   */
   FAT_KERNEL_PREFILL_4WAVE = 2,    /* 4 waves, 128 query rows per workgroup   */
   FAT_KERNEL_PREFILL_4WAVE_SPLIT = 3 /* 8 waves, 128 query rows: two 4-wave
                                         groups take alternate key tiles and
                                         merge (m, l, O) at the end          */
+};
+
+/* Row addressing of fat_prefill_paged (the `rows` field): AUTO picks the
+ * fastest form the page size allows; the others force one (tests check that
+ * all of them give identical bits). */
+enum fat_rows {
+  FAT_ROWS_AUTO = 0,
+  FAT_ROWS_WIDE = 1, /* wave-uniform page ids, 64-bit row addresses          */
+  FAT_ROWS_LANE = 2  /* per-lane page ids and row addresses (any page size)  */
 };
 
 /* Error codes. */
@@ -81,16 +95,21 @@ enum fat_status {
  * Paged decode: one query per sequence against a paged K/V cache.
  *
  * Layouts (NHD pages, flashattn_tile/paging.py:1-20):
- *   q        [batch, num_heads, head_dim]          q_dtype
+ *   q        [batch, num_heads, head_dim]          q_dtype (fp16, bf16, fp32)
  *   k_cache  [num_pages, page_size, num_kv_heads, head_dim]  kv_dtype
  *   v_cache  same shape and dtype as k_cache
  *   k_scale  [num_pages, num_kv_heads] fp32, only for int8/fp8 kv_dtype
  *   v_scale  same as k_scale
  *   page_table int32 [batch, max_pages]  (row stride page_table_stride)
- *   seq_lens int32 [batch], every entry in [1, max_pages*page_size]
- * page_size is a power of two of at least the rows one 16-byte load per lane
- * covers: 4 (fp16/bf16, head_dim 128), 8 (fp16/bf16 64; int8/fp8 128) or 16
- * (int8/fp8 64); smaller pages return FAT_E_UNSUPPORTED.
+ *   seq_lens int32 [batch]; a sequence of length <= 0 yields zeros, and
+ *            lengths beyond max_pages*page_size are clamped to it
+ * head_dim is 32, 64, 128 or 256 and page_size any positive number (page
+ * ids are clamped to [0, num_pages)).  The VALU and MFMA kernels take
+ * fp16/bf16 queries, head_dim 64 or 128 and power-of-two pages of at least
+ * the rows one 16-byte load per lane covers: 4 (fp16/bf16, head_dim 128), 8
+ * (fp16/bf16 64; int8/fp8 128) or 16 (int8/fp8 64).  Every other request
+ * runs on the generic kernel (one query per sequence only); fp32 queries
+ * take an fp32 cache.
  *   out      [batch, num_heads, head_dim]          q_dtype
  * Strides are in elements; the head_dim axis must be contiguous.
  *
@@ -138,8 +157,8 @@ typedef struct fat_decode_args {
   int32_t max_pages;
   int32_t split_k;
   int32_t waves_per_group; /* 0 = chosen by the library, else 4 or 8 */
-  int32_t q_dtype;  /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 (also the out dtype) */
-  int32_t kv_dtype; /* q_dtype, FAT_DTYPE_I8 or FAT_DTYPE_FP8E4M3           */
+  int32_t q_dtype;  /* FAT_DTYPE_F16, _BF16 or _F32 (also the out dtype)  */
+  int32_t kv_dtype; /* q_dtype, or FAT_DTYPE_I8 / _FP8E4M3 (16-bit q)    */
   int32_t pages_per_split; /* 0 = ceil(pages / split_k) per sequence        */
   float softmax_scale;
   /* Multi-token decode (q_len > 1): q and out are [batch, q_len, num_heads,
@@ -151,7 +170,7 @@ typedef struct fat_decode_args {
    * batch * q_len, ...).  At most 64 tokens. */
   int64_t q_stride_t, out_stride_t;
   int32_t q_len;
-  int32_t kernel; /* FAT_KERNEL_AUTO, _DECODE_VALU or _DECODE_MFMA */
+  int32_t kernel; /* FAT_KERNEL_AUTO, _DECODE_VALU, _MFMA or _GENERIC */
 } fat_decode_args;
 
 /*
@@ -235,6 +254,7 @@ typedef struct fat_prefill_paged_args {
   int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
   float softmax_scale;
   int32_t kernel; /* FAT_KERNEL_AUTO, _PREFILL_PINGPONG or _PREFILL_4WAVE */
+  int32_t rows;   /* FAT_ROWS_AUTO, _WIDE or _LANE                        */
 } fat_prefill_paged_args;
 
 /*
@@ -321,7 +341,7 @@ const char* fat_last_error(void);
 size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads,
                                         int32_t head_dim, int32_t split_k);
 
-/* Enqueue paged decode (fp16/bf16/int8/fp8 K/V) on `stream`.
+/* Enqueue paged decode (fp16/bf16/fp32/int8/fp8 K/V) on `stream`.
  * Replaces flashattn_tile/kernels/decode.py:533-704 (see file header). */
 int fat_paged_decode(const fat_decode_args* args, void* stream);
 

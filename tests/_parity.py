@@ -92,3 +92,32 @@ def make_varlen(lens, num_heads, num_kv_heads, head_dim, dtype, seed=0, scale=1.
     v = (torch.randn(total, num_kv_heads, head_dim, generator=g) * scale).to(dtype)
     cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0).tolist()), dtype=torch.int32)
     return q.to(device), k.to(device), v.to(device), cu.to(device)
+
+
+def force_decode_knobs(monkeypatch, **knobs):
+    """Make every decode wrapper call in this test launch with ``knobs``
+    (``kernel``, ``num_warps``) on top of the launch it resolves; the choice
+    reaches the library through the ``kernel`` / ``waves_per_group`` fields
+    of ``fat_decode_args``."""
+    import flashattntile_amd.kernels.decode as dec
+
+    resolve = dec._resolve_config
+
+    def forced(config, q, cache, max_len, total_pages, q_len=1):
+        return {**resolve(config, q, cache, max_len, total_pages, q_len), **knobs}
+
+    monkeypatch.setattr(dec, "_resolve_config", forced)
+
+
+def force_prefill_knobs(monkeypatch, **knobs):
+    """The same for the prefill wrappers (``kernel``, and ``rows`` for paged
+    prefill)."""
+    import flashattntile_amd.kernels.prefill as pre
+
+    resolve = pre._resolve_config
+
+    def forced(config, kind=None, signature=None, defaults=pre.DEFAULT_CONFIG):
+        cfg = resolve(config, kind, signature, defaults)
+        return {**cfg, **{k: v for k, v in knobs.items() if k in cfg}}
+
+    monkeypatch.setattr(pre, "_resolve_config", forced)

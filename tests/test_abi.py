@@ -103,19 +103,31 @@ def test_decode_argument_errors_are_reported():
     a.head_dim = 96
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "head_dim" in _err()
     a.head_dim = 128
-    a.page_size = 12
-    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "page_size" in _err()
-    a.page_size = 16
+    a.page_size = 0
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "page_size" in _err()
+    # pages of 2 rows exist only for the generic kernel
+    a.page_size, a.kernel = 2, _hip.KERNEL_DECODE_MFMA
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "GENERIC" in _err()
+    a.page_size, a.kernel = 16, _hip.KERNEL_AUTO
     a.kv_dtype = _hip.DT_I8
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "scale" in _err()
+    a.k_scale = a.v_scale = 0x2000
+    a.num_heads, a.kernel = 16, _hip.KERNEL_DECODE_VALU  # 8-bit cache, GQA group 8
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "VALU decode takes int8/fp8" in _err()
+    a.num_heads, a.kernel = 4, _hip.KERNEL_AUTO
+    a.q_dtype = _hip.DT_F32  # fp32 queries take an fp32 cache only
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "kv_dtype" in _err()
+    a.k_scale = a.v_scale = None
     a.kv_dtype = _hip.DT_F16
     a.q_dtype = 9
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "q_dtype" in _err()
     a.q_dtype = _hip.DT_F16
-    a.kernel = 3
+    a.kernel = 4
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "kernel" in _err()
     a.kernel, a.q_len = _hip.KERNEL_DECODE_VALU, 2
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "VALU" in _err()
+    a.kernel = _hip.KERNEL_DECODE_GENERIC  # one query per sequence only
+    assert lib.fat_paged_decode(ctypes.byref(a), None) == 2 and "multi-token" in _err()
     a.kernel, a.q_len = _hip.KERNEL_AUTO, 0
     a.k_stride_slot = 3  # 6-byte rows: misaligned for 16-byte loads
     assert lib.fat_paged_decode(ctypes.byref(a), None) == 1 and "aligned" in _err()
@@ -139,6 +151,8 @@ def test_prefill_argument_errors_are_reported():
     p.num_pages, p.max_pages = 1, 1
     p.kernel = -1
     assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "kernel" in _err()
+    p.kernel, p.rows = _hip.KERNEL_AUTO, 3
+    assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "rows" in _err()
 
 
 def test_quantize_argument_errors_are_reported():

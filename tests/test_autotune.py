@@ -176,15 +176,15 @@ def test_autotune_ranks_and_saves(tmp_path):
 
     import time as _time
 
-    real = _time.perf_counter
+    real = _time.perf_counter_ns
     try:
-        _time.perf_counter = lambda: clock["t"]  # deterministic CPU timing
+        _time.perf_counter_ns = lambda: int(clock["t"] * 1e9)  # deterministic CPU timing
         with pytest.warns(RuntimeWarning, match="skipped"):
             rows = at.autotune({"kind": "prefill", "signature": "S", "runner": runner, "flops": 4e9, "bytes": 2e9,
                                 "default": {"kernel": "a"}},
                                [{"kernel": k} for k in ("a", "b", "bad", "c")], warmup=1, iters=3, path=path)
     finally:
-        _time.perf_counter = real
+        _time.perf_counter_ns = real
     assert [r["kernel"] for r in rows] == ["b", "c", "a"] and [r["rank"] for r in rows] == [1, 2, 3]
     assert rows[0]["latency_ms"] == pytest.approx(1000.0) and rows[0]["gbytes_per_s"] == pytest.approx(2.0)
     assert at.best_config("prefill", "S", path=path) == {"kernel": "b"}

@@ -14,7 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _parity import assert_parity, make_paged
+from _parity import assert_parity, force_decode_knobs, make_paged
 from flashattntile_amd import PagedKVCache, paged_decode_attention, paged_decode_attention_fp8
 from flashattntile_amd.kernels.decode import paged_decode_attention_multi
 from flashattntile_amd.quant import quantize_cache
@@ -43,10 +43,10 @@ def _ref32(q, k, v, cache, scale=None):
 LENS = [40, 17, 255, 1000]
 
 
-@pytest.fixture(params=["4", "8"], autouse=True)
+@pytest.fixture(params=[4, 8], autouse=True)
 def mfma_waves(request, monkeypatch):
     """Every multi-token case on the MFMA decode with 4 and 8 waves."""
-    monkeypatch.setenv("FAT_DECODE_MFMA_WAVES", request.param)
+    force_decode_knobs(monkeypatch, num_warps=request.param)
     return request.param
 
 

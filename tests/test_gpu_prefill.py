@@ -12,7 +12,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _parity import assert_parity, make_varlen, ulp
+from _parity import assert_parity, force_prefill_knobs, make_varlen, ulp
 from flashattntile_amd import prefill_attention
 from flashattntile_amd.kernels.prefill import prefill_launch
 from oracle.reference import ref_attention_varlen
@@ -24,9 +24,11 @@ ODD_LENS = [1, 17, 255, 1000]
 
 @pytest.fixture(params=["auto", "pingpong", "4wave", "4wave_split"])
 def kernel(request, monkeypatch):
-    """Run the test with the library's automatic choice and with each of the
-    two prefill kernels forced (8-wave ping-pong, 4-wave), whatever the shape."""
-    monkeypatch.setenv("FAT_PREFILL_KERNEL", request.param)
+    """Run the test with the library's automatic choice and with each prefill
+    kernel forced (8-wave ping-pong, 4-wave, 4-wave key split), whatever the
+    shape."""
+    if request.param != "auto":
+        force_prefill_knobs(monkeypatch, kernel=request.param)
     return request.param
 
 

@@ -14,7 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _parity import assert_parity, make_paged
+from _parity import assert_parity, force_prefill_knobs, make_paged
 from flashattntile_amd import PagedKVCache
 from flashattntile_amd.kernels.prefill import paged_prefill_attention, prefill_attention
 from flashattntile_amd.paging import gather_contiguous
@@ -26,7 +26,8 @@ DEV = "cuda"
 
 @pytest.fixture(params=["auto", "pingpong", "4wave", "4wave_split"])
 def kernel(request, monkeypatch):
-    monkeypatch.setenv("FAT_PREFILL_KERNEL", request.param)
+    if request.param != "auto":
+        force_prefill_knobs(monkeypatch, kernel=request.param)
     return request.param
 
 
@@ -130,7 +131,7 @@ def test_paged_prefill_validation():
 
 
 @pytest.mark.parametrize("P", [16, 32, 64])
-def test_paged_prefill_row_modes_agree(P, monkeypatch):
+def test_paged_prefill_row_modes_agree(P):
     """Pages of >= 16 rows take the wave-uniform addressing (32-bit pool
     offsets for a pool under 2 GiB); forcing 64-bit row addresses or the
     per-lane addressing on the same inputs must give identical bits."""
@@ -138,10 +139,8 @@ def test_paged_prefill_row_modes_agree(P, monkeypatch):
     lens_k, lens_q = [900, 70, 129], [300, 70, 1]
     q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, P, torch.bfloat16, seed=P + 1)
     uni = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
-    monkeypatch.setenv("FAT_PREFILL_PAGED_ROWS", "wide")
-    wide = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
-    monkeypatch.setenv("FAT_PREFILL_PAGED_ROWS", "lane")
-    lane = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    wide = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, config={"rows": "wide"})
+    lane = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, config={"rows": "lane"})
     torch.cuda.synchronize()
     assert torch.equal(uni, lane) and torch.equal(uni, wide)
     assert_parity(uni, _ref32(q, cache, cu, True), label=f"paged P{P} uniform rows")

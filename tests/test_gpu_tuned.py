@@ -1,10 +1,10 @@
 """GPU tests of the per-launch kernel choice (ABI field ``kernel``) and of
 the gfx950 tuned-config store routing ``config=None`` launches.
 
-A launch forced through the config is the same launch as one forced through
-the environment variables the other GPU tests use, so its output must be
-bit-identical; a launch taken from the store must be bit-identical to the
-same config passed explicitly.  Parity against the fp32 oracle (2e-3,
+A launch forced through the config reaches the library as the ``kernel``
+field (the library reads no environment); the library's own choice must be
+bit-identical to the forced kernel it picks, and a launch taken from the
+store must be bit-identical to the same config passed explicitly.  Parity against the fp32 oracle (2e-3,
 tests/_parity.py) is checked once per kernel.
 """
 
@@ -19,7 +19,7 @@ from _parity import assert_parity, make_paged, make_query, make_varlen
 from flashattntile_amd import (PagedKVCache, paged_decode_attention, paged_decode_attention_multi,
                                paged_prefill_attention, prefill_attention)
 from flashattntile_amd import autotune as at
-from oracle.reference import ref_attention_paged, ref_attention_varlen
+from oracle.reference import ref_attention_paged, ref_attention_paged_prefill, ref_attention_varlen
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -31,22 +31,22 @@ def _decode_case(lens, h, hk, dtype, seed):
     return make_query(len(lens), h, 128, dtype, seed=seed + 1, device=DEV), PagedKVCache(k, v, pt, sl, 16)
 
 
-@pytest.mark.parametrize("kern", ["valu", "mfma"])
 @pytest.mark.parametrize("h,hk", [(32, 8), (8, 2), (32, 1)])
-def test_decode_kernel_config_equals_env_forcing(kern, h, hk, monkeypatch):
-    label = f"decode kernel={kern} H{h}/{hk}"
+def test_decode_kernel_field_selects_the_kernel(h, hk):
+    """Each forced kernel passes parity, and the library's own choice is
+    bit-identical to one of them (VALU for groups below 8, MFMA from 8)."""
+    label = f"decode kernel field H{h}/{hk}"
     print(label, flush=True)
     q, cache = _decode_case(LENS, h, hk, torch.bfloat16, seed=h + hk)
-    out_cfg = paged_decode_attention(q, cache, config={"split_k": 4, "kernel": kern})
-    monkeypatch.setenv("FAT_DECODE_KERNEL", "mfma" if kern == "valu" else "valu")  # the field wins over it
-    out_cfg2 = paged_decode_attention(q, cache, config={"split_k": 4, "kernel": kern})
-    monkeypatch.setenv("FAT_DECODE_KERNEL", kern)
-    out_env = paged_decode_attention(q, cache, config={"split_k": 4})
-    torch.cuda.synchronize()
-    assert torch.equal(out_cfg, out_env) and torch.equal(out_cfg2, out_env), label
     ref = ref_attention_paged(q.cpu(), cache.k_cache.cpu(), cache.v_cache.cpu(), cache.page_table.cpu(),
                               cache.seq_lens.cpu(), return_fp32=True)
-    assert_parity(out_cfg, ref, label=label)
+    outs = {kern: paged_decode_attention(q, cache, config={"split_k": 4, "kernel": kern})
+            for kern in ("valu", "mfma", "generic")}
+    auto = paged_decode_attention(q, cache, config={"split_k": 4})
+    torch.cuda.synchronize()
+    for kern, out in outs.items():
+        assert_parity(out, ref, label=f"{label} {kern}")
+    assert torch.equal(auto, outs["valu" if h // hk < 8 else "mfma"]), label
 
 
 def test_multi_token_decode_kernel_choice():
@@ -63,28 +63,28 @@ def test_multi_token_decode_kernel_choice():
 
 
 @pytest.mark.parametrize("kern", ["pingpong", "4wave", "4wave_split"])
-def test_prefill_kernel_config_equals_env_forcing(kern, monkeypatch):
+def test_prefill_kernel_field_selects_the_kernel(kern):
+    """A forced prefill kernel passes parity, packed and paged, and the
+    library's own choice for this shape (ping-pong: 384 blocks of 256 rows)
+    is bit-identical to forcing it."""
     label = f"prefill kernel={kern}"
     print(label, flush=True)
     lens = [1, 255, 1000]
     q, k, v, cu = make_varlen(lens, 32, 8, 128, torch.float16, seed=11, device=DEV)
     out_cfg = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True, config={"kernel": kern})
-    monkeypatch.setenv("FAT_PREFILL_KERNEL", kern)
-    out_env = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True)
+    auto = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=True, config={})
     torch.cuda.synchronize()
-    assert torch.equal(out_cfg, out_env), label
+    if kern == "pingpong":
+        assert torch.equal(out_cfg, auto), label
     ref = ref_attention_varlen(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), causal=True, return_fp32=True)
     assert_parity(out_cfg, ref, label=label)
-    # the paged prefill takes the same knob
     kc, vc, pt, sl = make_paged(lens, 8, 128, 16, torch.float16, seed=12, device=DEV)
     cache = PagedKVCache(kc, vc, pt, sl, 16)
     p_cfg = paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
-    monkeypatch.setenv("FAT_PREFILL_KERNEL", "4wave" if kern == "pingpong" else "pingpong")
-    p_cfg2 = paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
-    monkeypatch.setenv("FAT_PREFILL_KERNEL", kern)
-    p_env = paged_prefill_attention(q, cache, cu, max(lens))
     torch.cuda.synchronize()
-    assert torch.equal(p_cfg, p_env) and torch.equal(p_cfg2, p_env), label
+    ref_p = ref_attention_paged_prefill(q.cpu(), kc.cpu(), vc.cpu(), pt.cpu(), sl.cpu(), cu.cpu(), causal=True,
+                                        return_fp32=True)
+    assert_parity(p_cfg, ref_p, label=f"paged {label}")
 
 
 def test_store_routes_config_none_launches(tmp_path, monkeypatch):
