@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # enum fat_dtype
 DT_F16 = 0
@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "fat_last_error",
     "fat_paged_decode_workspace_bytes",
     "fat_paged_decode",
+    "fat_paged_decode_noalloc",
     "fat_prefill_workspace_bytes",
     "fat_prefill_varlen",
     "fat_prefill_paged",
@@ -277,6 +278,8 @@ def _load() -> None:
         lib.fat_paged_decode_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32, _c_i32]
         lib.fat_paged_decode.restype = ctypes.c_int
         lib.fat_paged_decode.argtypes = [ctypes.POINTER(DecodeArgs), _c_vp]
+        lib.fat_paged_decode_noalloc.restype = ctypes.c_int
+        lib.fat_paged_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _c_vp]
         lib.fat_prefill_workspace_bytes.restype = ctypes.c_size_t
         lib.fat_prefill_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32]
         lib.fat_prefill_varlen.restype = ctypes.c_int
@@ -440,6 +443,16 @@ def decode_args(
 def decode_with_args(a: DecodeArgs, stream: int) -> None:
     """Enqueue ``fat_paged_decode`` with a prepared argument block."""
     _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(stream)), "fat_paged_decode")
+
+
+# FAT_DECODE_NOALLOC_MAX_WORKSPACE of include/fat_abi.h
+NOALLOC_MAX_WORKSPACE = 32 << 20
+
+
+def decode_noalloc_with_args(a: DecodeArgs, stream: int) -> None:
+    """Enqueue ``fat_paged_decode_noalloc`` (split-K workspace inside the
+    library; ``a.workspace`` is ignored) with a prepared argument block."""
+    _check(lib().fat_paged_decode_noalloc(ctypes.byref(a), _c_vp(stream)), "fat_paged_decode_noalloc")
 
 
 def prefill_varlen(

@@ -35,6 +35,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "decode_params.h"
@@ -1116,4 +1117,72 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   if (rc != FAT_OK || a->split_k == 1) return rc;
 
   return launch_merge(prm, a, D, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split-K workspace lives in a file-scope device
+// array instead of caller memory.  Every GPU the library runs on holds its
+// own copy of `scratch` (kScratchBytes) until the process ends.  Its device
+// address is looked up once per device with hipGetSymbolAddress (the array's
+// name is only a host-side stand-in) and used for every launch after that.
+// Nothing in it needs clearing: each partition of a launch writes its whole
+// (acc, m, l) row before the merge reads it.  Two calls that overlap on one
+// GPU (different streams) share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = FAT_DECODE_NOALLOC_MAX_WORKSPACE;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+}  // namespace
+
+extern "C" int fat_paged_decode_noalloc(const fat_decode_args* a, void* stream) {
+  fat_host::clear_error();
+  if (!a) {
+    fat_host::set_error("fat_paged_decode_noalloc: args is NULL");
+    return FAT_E_INVALID;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fat_host::set_error("fat_paged_decode_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
+    return FAT_E_INVALID;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) {
+    fat_host::set_error("fat_paged_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(g_scratch_err[dev]));
+    return FAT_E_LAUNCH;
+  }
+  if (a->batch <= 0 || a->num_heads <= 0 || a->head_dim <= 0 || a->split_k < 1 || a->q_len < 0) {
+    return fat_paged_decode(a, stream);  // the regular entry reports the bad argument
+  }
+  const int64_t rows = (int64_t)a->batch * (a->q_len > 1 ? a->q_len : 1);
+  const size_t need = a->split_k > 1 ? (size_t)rows * a->num_heads * a->split_k * (a->head_dim + 2) * sizeof(float)
+                                     : 0;
+  if (need > kScratchBytes) {
+    fat_host::set_error("fat_paged_decode_noalloc: this launch needs %zu bytes of split-K workspace; the "
+                        "allocation-free entry holds at most %zu (lower split_k, or use fat_paged_decode with a "
+                        "workspace)", need, kScratchBytes);
+    return FAT_E_INVALID;
+  }
+  fat_decode_args b = *a;
+  b.workspace = need ? g_scratch_ptr[dev] : nullptr;
+  const int rc = fat_paged_decode(&b, stream);
+  if (rc != FAT_OK) {
+    // Name this entry in the message the shared path set.
+    char msg[480];
+    snprintf(msg, sizeof(msg), "%s", fat_last_error());
+    fat_host::set_error("fat_paged_decode_noalloc: %s", msg);
+  }
+  return rc;
 }

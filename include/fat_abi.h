@@ -43,10 +43,11 @@
 extern "C" {
 #endif
 
-/* 8: fp32 decode, any page size and head_dim 32/256 through the generic
+/* 9: fat_paged_decode_noalloc (allocation-free decode).
+ * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 8
+#define FAT_ABI_VERSION 9
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -344,6 +345,20 @@ size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads,
 /* Enqueue paged decode (fp16/bf16/fp32/int8/fp8 K/V) on `stream`.
  * Replaces flashattn_tile/kernels/decode.py:533-704 (see file header). */
 int fat_paged_decode(const fat_decode_args* args, void* stream);
+
+/* Allocation-free paged decode.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  The same launch as
+ * fat_paged_decode(args, stream), except that the split-K workspace is a
+ * device array inside the library (FAT_DECODE_NOALLOC_MAX_WORKSPACE bytes
+ * per GPU, held until the process ends); args->workspace is ignored.  The
+ * library allocates and frees nothing.  A launch whose workspace
+ * (fat_paged_decode_workspace_bytes of its batch * q_len rows) exceeds the
+ * maximum returns FAT_E_INVALID.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (e.g. on two streams) race.  The
+ * current HIP device must be the one `stream` belongs to. */
+#define FAT_DECODE_NOALLOC_MAX_WORKSPACE ((size_t)32 << 20)
+int fat_paged_decode_noalloc(const fat_decode_args* args, void* stream);
 
 /* Bytes of workspace fat_prefill_varlen needs. */
 size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
