@@ -292,9 +292,12 @@ def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7)
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
     mx = max(lens)
+    # the workspace the product path (kernels/prefill.py:prefill_launch) passes
+    need = _hip.prefill_workspace_bytes(k.shape[0], hkv, d) if dtype == torch.bfloat16 else 0
+    ws = torch.empty(need, dtype=torch.uint8, device=device) if need else None
 
     def step(i):
-        _hip.prefill_varlen(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, stream=handle)
+        _hip.prefill_varlen(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, workspace=ws, stream=handle)
 
     ms = _time_steps(step, steps, warmup, stream)
     flops = flops_attention_varlen(hq, d, lens, lens, causal=True)

@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # enum fat_dtype
 DT_F16 = 0

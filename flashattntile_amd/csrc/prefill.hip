@@ -73,6 +73,9 @@ struct PrefillParams {
   int64_t k_sp, v_sp;   // page strides (elements)
   int32_t pshift;       // log2(page_size)
   int32_t num_pages, max_pages;
+  // bf16 V converted ahead of the kernel (VPRE instantiations): v points at
+  // fp16 values scaled by 2^-v_head_scale[kv head].
+  const int32_t* v_head_scale;
 };
 
 constexpr int kBM = 128;
@@ -609,7 +612,10 @@ void prefill_kernel(const PrefillParams p) {
           const float x1 = fast_exp2(__builtin_fmaf(s_cur[jb][8 * t + 2 * e2 + 1], cm, nmo));
           // P^T operand: k-step t of key block jb uses accumulator regs 8t..8t+7.
           pf[jb][t][e2] = Pair<F16>::pack(x0, x1);
-          lsq[t][e2 >> 1] += x0 + x1;  // fp32 adds: v_dot2 would stall the other wave's MFMAs
+          // fp32 adds (v_dot2 would stall the other wave's MFMAs); the first
+          // pair of each partial sum is assigned, not added to 0.
+          if (jb == 0 && (e2 & 1) == 0) lsq[t][e2 >> 1] = x0 + x1;
+          else lsq[t][e2 >> 1] += x0 + x1;
         }
     l_run += (lsq[0][0] * back[0][0] + lsq[0][1] * back[0][1]) + (lsq[1][0] * back[1][0] + lsq[1][1] * back[1][1]);
 
@@ -741,7 +747,7 @@ struct MfmaPhaseOrder {
 constexpr float kLazyPP = 15.0f;
 constexpr float kLazyPPSum = 32768.0f;  // 2^kLazyPP
 
-template <typename T, int D, bool CAUSAL, bool POS, int PG>
+template <typename T, int D, bool CAUSAL, bool POS, int PG, bool VPRE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;
@@ -763,6 +769,10 @@ void prefill_pp_kernel(const PrefillParams p) {
   // <= 2^-25 * 2^s); vsc[buffer][wave] holds s.  The softmax folds
   // 2^(s - e_acc) into P's exponent, where O is kept as acc * 2^e_acc.
   constexpr bool VH = std::is_same<T, BF16>::value;
+  // VPRE: V arrives as fp16 already, scaled by one power of two per KV head
+  // (bf16v_to_f16_kernel), so staging is a plain copy and every wave's scale
+  // is the head's.
+  static_assert(!VPRE || (VH && PG == 0), "V pre-conversion is for packed bf16 prefill");
   __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
   const int per = p.B * p.H;
@@ -827,6 +837,7 @@ void prefill_pp_kernel(const PrefillParams p) {
   uint16_t* const lds0 = grp ? &Vs[0][0] : &Ks[0][0];
   const int lds_buf = grp ? kBN * V_RS : kBN * K_RS;
   const int lds_off = (gt / CPR) * lds_rs + 8 * (gt % CPR);
+  const int vpre_sw = VPRE ? p.v_head_scale[kvh] : 0;
   u32x4 stage[LOADS];
   // PAGED only: this group's K or V stream (PG 1 per-lane page ids, PG 2
   // wave-uniform ones).
@@ -865,7 +876,9 @@ void prefill_pp_kernel(const PrefillParams p) {
   };
   auto lstore = [&](int buf) {
     if constexpr (PG >= 2) pr.mask_tail(stage);
-    if constexpr (VH) {
+    if constexpr (VPRE) {
+      if (grp == 1 && lane == 0) vsc[buf][w - 4] = vpre_sw;
+    } else if constexpr (VH) {
       if (grp == 1) {
         const int sw = bf16_to_f16_scaled<LOADS>(stage);
         if (lane == 0) vsc[buf][w - 4] = sw;
@@ -975,8 +988,14 @@ void prefill_pp_kernel(const PrefillParams p) {
             pf[jb][tt][e2] = Pair<F16>::pack(x0, x1);
             // fp32 adds, not v_dot2: a dot2 on one wave stalls the other
             // wave's MFMAs (measured on gfx950), undoing the ping-pong overlap.
-            if constexpr (VH) lsq[tt][e2 >> 1] += x0 + x1;
-            else lsq[jb][tt] += x0 + x1;
+            // (the first pair of each partial sum is assigned, not added to 0)
+            if constexpr (VH) {
+              if (jb == 0 && (e2 & 1) == 0) lsq[tt][e2 >> 1] = x0 + x1;
+              else lsq[tt][e2 >> 1] += x0 + x1;
+            } else {
+              if (e2 == 0) lsq[jb][tt] = x0 + x1;
+              else lsq[jb][tt] += x0 + x1;
+            }
           }
       if constexpr (VH)
         return (lsq[0][0] * back[0][0] + lsq[0][1] * back[0][1]) + (lsq[1][0] * back[1][0] + lsq[1][1] * back[1][1]);
@@ -1083,6 +1102,77 @@ void prefill_pp_kernel(const PrefillParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 V conversion ahead of the ping-pong kernel (VPRE).  The kernel's PV
+// product is one fp16 MFMA with P rounded to fp16; bf16 V must therefore be
+// staged as fp16.  Converting it inside the kernel costs each group-B wave
+// ~80 VALU instructions per tile; converting it once beforehand costs one
+// read and one write of V.  One power of two per KV head keeps every value
+// inside fp16's range: 2^-s with s = 0 unless some |v| >= 2^15 (then s = the
+// head's largest exponent - 14).  Values are exact apart from fp16
+// subnormals (absolute error <= 2^-25 * 2^s), as in the in-kernel form.
+// ---------------------------------------------------------------------------
+constexpr int kVpreRows = 64;  // V rows per pre-pass workgroup
+
+// Largest bf16 exponent field of |v| over rows [blk * 64, blk * 64 + 64) of
+// KV head h -> blockmax[h * nblk + blk].
+template <int D>
+__global__ __launch_bounds__(256) void bf16v_expmax_kernel(const uint16_t* __restrict__ v, int64_t v_st,
+                                                           int64_t v_sh, int total_k, int nblk,
+                                                           int32_t* __restrict__ blockmax) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  const int blk = blockIdx.x;
+  const int h = blockIdx.y;
+  u32 em = 0;
+  for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
+    const int row = blk * kVpreRows + c / CPR;
+    if (row < total_k) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) em = max(em, max(x[e] & 0x7f80u, (x[e] >> 16) & 0x7f80u));
+    }
+  }
+  __shared__ u32 red[4];
+  u32 m = em;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (u32)__shfl_xor((int)m, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) blockmax[h * nblk + blk] = (int32_t)(max(max(red[0], red[1]), max(red[2], red[3])) >> 7);
+}
+
+// fp16(v * 2^-s_h) of rows [blk * 64, blk * 64 + 64) of KV head h into the
+// dense [total_k, Hkv, D] array v16; workgroup (0, h) records s_h.
+template <int D>
+__global__ __launch_bounds__(256) void bf16v_to_f16_kernel(const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
+                                                           int total_k, int Hkv, int nblk,
+                                                           const int32_t* __restrict__ blockmax,
+                                                           uint16_t* __restrict__ v16, int32_t* __restrict__ head_scale) {
+  constexpr int CPR = D / 8;
+  const int blk = blockIdx.x;
+  const int h = blockIdx.y;
+  int le = 0;
+  for (int i = threadIdx.x; i < nblk; i += 256) le = max(le, blockmax[h * nblk + i]);
+  __shared__ int red[4];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) le = max(le, __shfl_xor(le, off));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = le;
+  __syncthreads();
+  le = max(max(red[0], red[1]), max(red[2], red[3]));
+  const int sw = max(0, le - 141);  // 2^(le - 127) >= 2^15 <=> le >= 142
+  if (blk == 0 && threadIdx.x == 0) head_scale[h] = sw;
+  const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 128
+  for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
+    const int row = blk * kVpreRows + c / CPR;
+    if (row >= total_k) continue;
+    const u32x4 x = *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
+    u32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = Pair<F16>::pack(Pair<BF16>::lo(x[e]) * f, Pair<BF16>::hi(x[e]) * f);
+    *reinterpret_cast<u32x4*>(v16 + ((int64_t)row * Hkv + h) * D + 8 * (c % CPR)) = y;
+  }
+}
+
 }  // namespace fat
 
 // ===========================================================================
@@ -1099,22 +1189,34 @@ void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStr
   }
 }
 
-template <typename T, int D, bool CAUSAL, int PG>
+template <typename T, int D, bool CAUSAL, int PG, bool VPRE = false>
 void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
   if (pos) {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true, PG>), grid, dim3(512), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true, PG, VPRE>), grid, dim3(512), 0, stream, prm);
   } else {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false, PG>), grid, dim3(512), 0, stream, prm);
+    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false, PG, VPRE>), grid, dim3(512), 0, stream, prm);
   }
 }
 
 // Kernel families of the prefill launch.
 enum PrefillKind { PF_PINGPONG, PF_4WAVE, PF_4WAVE_SPLIT };
 
+// Bytes of the fp16 copy of V in the prefill workspace (256-byte aligned).
+size_t vpre_bytes_v16(int64_t total_k, int64_t hkv, int64_t d) {
+  return (size_t)((total_k * hkv * d * 2 + 255) / 256 * 256);
+}
+
 template <typename T, int D, int PG>
 int launch_prefill_t(const fat::PrefillParams& prm, bool causal, PrefillKind kind, dim3 grid, hipStream_t stream) {
   const bool pos = prm.scale_log2 > 0.f;
   if (kind == PF_PINGPONG) {
+    if constexpr (std::is_same<T, fat::BF16>::value && PG == 0) {
+      if (prm.v_head_scale) {
+        if (causal) launch_prefill_pp_c<T, D, true, PG, true>(prm, pos, grid, stream);
+        else launch_prefill_pp_c<T, D, false, PG, true>(prm, pos, grid, stream);
+        return fat_host::launch_status("prefill_pp_kernel");
+      }
+    }
     if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
     else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
     return fat_host::launch_status("prefill_pp_kernel");
@@ -1151,7 +1253,8 @@ bool valid_prefill_kernel(int kernel) {
 // tests run every kernel on every shape that way).
 template <int PG>
 int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
-                   float softmax_scale, int kernel, const char* who, hipStream_t stream) {
+                   float softmax_scale, int kernel, const char* who, hipStream_t stream, void* workspace = nullptr,
+                   int total_k = 0) {
   const int64_t heads = (int64_t)prm.B * prm.H;
   const int64_t n_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM * heads;
   const int64_t n_4w = (max_seqlen_q + fat::kBM - 1) / fat::kBM * heads;
@@ -1175,6 +1278,37 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     return FAT_E_UNSUPPORTED;
   }
   const dim3 grid((unsigned)n);
+  // Packed bf16 on the ping-pong kernel: convert V to fp16 first when the
+  // caller gave the workspace (and the dense fp16 copy keeps the kernel's
+  // 32-bit per-sequence offsets).
+  prm.v_head_scale = nullptr;
+  if (PG == 0 && dtype == FAT_DTYPE_BF16 && kind == PF_PINGPONG && workspace && total_k > 0 &&
+      (int64_t)max_seqlen_k * 2 * prm.Hkv * D < 0x7fffffffLL && 2 * prm.Hkv * D < (1 << 24)) {
+    const int nblk = (total_k + fat::kVpreRows - 1) / fat::kVpreRows;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint16_t* v16 = reinterpret_cast<uint16_t*>(ws);
+    int32_t* blockmax = reinterpret_cast<int32_t*>(ws + vpre_bytes_v16(total_k, prm.Hkv, D));
+    int32_t* head_scale = blockmax + (int64_t)prm.Hkv * nblk;
+    const dim3 pgrid((unsigned)nblk, (unsigned)prm.Hkv);
+    const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(prm.v);
+    if (D == 128) {
+      hipLaunchKernelGGL((fat::bf16v_expmax_kernel<128>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, nblk, blockmax);
+      hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<128>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+    } else {
+      hipLaunchKernelGGL((fat::bf16v_expmax_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, nblk, blockmax);
+      hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+    }
+    const int rc = fat_host::launch_status("bf16v_to_f16_kernel");
+    if (rc != FAT_OK) return rc;
+    prm.v = reinterpret_cast<const uint8_t*>(v16);
+    prm.v_st = (int64_t)prm.Hkv * D;
+    prm.v_sh = D;
+    prm.v_head_scale = head_scale;
+  }
   if (dtype == FAT_DTYPE_F16) {
     return D == 128 ? launch_prefill_t<fat::F16, 128, PG>(prm, causal, kind, grid, stream)
                     : launch_prefill_t<fat::F16, 64, PG>(prm, causal, kind, grid, stream);
@@ -1186,10 +1320,9 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
 }  // namespace
 
 extern "C" size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads, int32_t head_dim) {
-  (void)total_k;
-  (void)num_kv_heads;
-  (void)head_dim;
-  return 0;  // V is transposed on the fly (ds_read_b64_tr_b16); no staging copy
+  if (total_k <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  const size_t nblk = ((size_t)total_k + fat::kVpreRows - 1) / fat::kVpreRows;
+  return vpre_bytes_v16(total_k, num_kv_heads, head_dim) + (nblk + 1) * (size_t)num_kv_heads * sizeof(int32_t);
 }
 
 extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
@@ -1267,8 +1400,13 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   prm.H = a->num_heads;
   prm.Hkv = a->num_kv_heads;
   prm.group = a->num_heads / a->num_kv_heads;
+  if (a->workspace && ((uintptr_t)a->workspace & 255)) {
+    fat_host::set_error("fat_prefill_varlen: workspace must be 256-byte aligned");
+    return FAT_E_INVALID;
+  }
   return launch_prefill<0>(prm, a->max_seqlen_q, a->max_seqlen_k, a->dtype, D, a->causal != 0, a->softmax_scale,
-                           a->kernel, "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr));
+                           a->kernel, "fat_prefill_varlen", static_cast<hipStream_t>(stream_ptr), a->workspace,
+                           a->total_k);
 }
 
 extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_ptr) {

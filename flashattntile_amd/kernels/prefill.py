@@ -148,7 +148,9 @@ def prefill_launch(
         raise ValueError("q, k, v need a contiguous head_dim axis")
     if out is None:
         out = torch.empty_like(q)
-    need = _hip.prefill_workspace_bytes(k.shape[0], k.shape[1], k.shape[2])
+    # bf16 takes a workspace for the fp16 copy of V the large-grid kernel
+    # stages (fp16 needs none); without one the kernel converts V itself.
+    need = _hip.prefill_workspace_bytes(k.shape[0], k.shape[1], k.shape[2]) if q.dtype == torch.bfloat16 else 0
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     # The kernels read cu_seqlens densely.

@@ -43,11 +43,13 @@
 extern "C" {
 #endif
 
-/* 9: fat_paged_decode_noalloc (allocation-free decode).
+/* 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
+ *     uses the workspace for an fp16 copy of V (optional).
+ * 9: fat_paged_decode_noalloc (allocation-free decode).
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 9
+#define FAT_ABI_VERSION 10
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -183,8 +185,12 @@ typedef struct fat_decode_args {
  *   out [total_q, num_heads, head_dim]      dtype
  * Causal masking is bottom-right aligned: query i of a sequence sees key j
  * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
- * fat_prefill_workspace_bytes() returns 0: the kernels need no workspace
- * (V is read key-major and transposed in LDS), so `workspace` may be NULL.
+ * `workspace` is optional (NULL, or 256-byte aligned and holding
+ * fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim) bytes).
+ * fp16 ignores it.  With bf16 the large-grid kernel then stages an fp16
+ * copy of V written there by a pre-pass (one power-of-two scale per KV
+ * head; results within the same bound as the in-kernel conversion it
+ * replaces); without it the kernel converts V tile by tile.
  */
 typedef struct fat_prefill_args {
   const void* q;
@@ -360,7 +366,7 @@ int fat_paged_decode(const fat_decode_args* args, void* stream);
 #define FAT_DECODE_NOALLOC_MAX_WORKSPACE ((size_t)32 << 20)
 int fat_paged_decode_noalloc(const fat_decode_args* args, void* stream);
 
-/* Bytes of workspace fat_prefill_varlen needs. */
+/* Bytes of the optional fat_prefill_varlen workspace (used by bf16). */
 size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
                                    int32_t head_dim);
 

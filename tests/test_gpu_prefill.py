@@ -140,8 +140,11 @@ def test_ops_compile_on_device():
 
 @pytest.mark.parametrize("huge", [7.0e4, 1.0e6, 3.0e8])
 def test_prefill_bf16_v_beyond_fp16_range(huge, kernel):
-    """bf16 V rows of magnitude >= 2^15 (the 8-wave kernel stages such a
-    staging wave's rows as fp16 scaled by 2^-s and tracks O as acc * 2^e).
+    """bf16 V rows of magnitude >= 2^15: V is staged as fp16 scaled by 2^-s
+    (per staging wave in the 4-wave kernels and in the ping-pong kernel
+    without a workspace; per KV head from the pre-pass when the ping-pong
+    kernel has one, as prefill_attention gives it) and O is tracked as
+    acc * 2^e.
     Key 300 (tile 4) holds huge/8 and the last two keys +-huge, so the scale
     grows twice along the sequence; queries before key 300 never see a huge
     row but read rows staged by the same wave (tile 4), which must keep the
@@ -165,3 +168,37 @@ def test_prefill_bf16_v_beyond_fp16_range(huge, kernel):
     excess = ((o32 - r32).abs() - rounding) / scale
     print(f"{label}: max relative error beyond rounding {excess.max().item():.3e}", flush=True)
     assert torch.isfinite(o32).all() and excess.max().item() <= 2e-3, label
+
+
+def test_prefill_bf16_with_and_without_workspace():
+    """bf16 on the ping-pong kernel with the workspace (V converted to fp16
+    by the pre-pass, one scale per KV head) and without it (V converted tile
+    by tile in the kernel): bit-identical while every |v| < 2^15 (both scales
+    are 1), and both within the tolerance when a row reaches 1e6."""
+    from flashattntile_amd import _hip
+
+    print("prefill bf16 workspace / no workspace", flush=True)
+    L = 1500
+    q, k, v, cu = make_varlen([L], 32, 8, 128, torch.bfloat16, seed=31, device=DEV)
+    outs = []
+    for big in (False, True):
+        if big:
+            v[700, 3] = 1.0e6
+        with_ws = prefill_launch(q, k, v, cu, cu, L, L, True, 128 ** -0.5, kernel="pingpong")
+        no_ws = torch.empty_like(q)
+        _hip.prefill_varlen(q, k, v, cu, cu, no_ws, L, L, True, 128 ** -0.5, workspace=None,
+                            kernel=_hip.KERNEL_PREFILL_PINGPONG)
+        torch.cuda.synchronize()
+        outs.append((with_ws, no_ws))
+    assert torch.equal(outs[0][0], outs[0][1])
+    for kvh in (0, 3):
+        hs = slice(4 * kvh, 4 * kvh + 4)
+        ref = _ref32(q[:, hs].contiguous(), k[:, kvh:kvh + 1].contiguous(), v[:, kvh:kvh + 1].contiguous(), cu, cu,
+                     True)
+        for name, out in zip(("workspace", "no workspace"), outs[1]):
+            o32, r32 = out[:, hs].float().cpu(), ref.float()
+            scale = r32.abs().amax(dim=-1, keepdim=True).clamp_min(1.0)
+            rounding = 0.5 * ulp(torch.maximum(o32.abs(), r32.abs()), torch.bfloat16)
+            excess = ((o32 - r32).abs() - rounding) / scale
+            print(f"kv{kvh} {name}: max relative error beyond rounding {excess.max().item():.3e}", flush=True)
+            assert torch.isfinite(o32).all() and excess.max().item() <= 2e-3, (kvh, name)
