@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 10
 
 # enum fat_dtype
 DT_F16 = 0
@@ -104,7 +104,6 @@ class DecodeArgs(ctypes.Structure):
         ("out_stride_t", _c_i64),
         ("q_len", _c_i32),
         ("kernel", _c_i32),
-        ("split_counters", _c_vp),
     ]
 
 
@@ -354,44 +353,6 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else int(t.data_ptr())
 
 
-# Split-K ticket counters (fat_decode_args.split_counters), one zeroed int32
-# buffer per (device, stream): launches on one stream run one after another,
-# and each completed launch leaves its counters zero for the next.
-_COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
-_COUNTERS_LOCK = threading.Lock()
-COUNTERS_DEFAULT = object()  # paged_decode: take the stream's buffer
-
-
-def decode_ticket_count(batch: int, num_heads: int, q_len: int = 1) -> int:
-    """Ticket counters a split-K launch may use: batch * q_len * num_heads."""
-    return int(batch) * max(int(q_len), 1) * int(num_heads)
-
-
-def stream_counters(device: torch.device, stream: int, count: int) -> torch.Tensor | None:
-    """The zeroed ticket counters reserved for launches on ``stream`` (a
-    hipStream_t handle), at least ``count`` of them; None while a graph is
-    being captured and the stream has none yet (the launch then merges its
-    partitions with a second kernel instead of allocating inside the
-    capture).  A new or grown buffer is zeroed and the device synchronised
-    before it is handed out, so no launch on another stream can see the fill
-    unfinished or the old buffer freed early."""
-    if count <= 0:
-        return None
-    dev = device.index if device.index is not None else torch.cuda.current_device()
-    key = (dev, int(stream))
-    with _COUNTERS_LOCK:
-        buf = _COUNTERS.get(key)
-        if buf is not None and buf.numel() >= count:
-            return buf
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        torch.cuda.synchronize(dev)
-        buf = torch.zeros(max(count, 4096), dtype=torch.int32, device=torch.device("cuda", dev))
-        torch.cuda.synchronize(dev)
-        _COUNTERS[key] = buf
-        return buf
-
-
 def paged_decode(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -409,24 +370,15 @@ def paged_decode(
     waves_per_group: int = 0,
     pages_per_split: int = 0,
     kernel: int = KERNEL_AUTO,
-    counters=COUNTERS_DEFAULT,
 ) -> None:
     """Enqueue ``fat_paged_decode`` for already-validated device tensors.
 
     ``q``/``out`` are ``[B, H, D]`` (one query per sequence) or
-    ``[B, T, H, D]`` (multi-token decode, ``q_len = T``).  With split_k > 1
-    the partitions are merged inside the launch through ``counters`` (by
-    default the stream's buffer, :func:`stream_counters`); ``counters=None``
-    merges them with a second kernel."""
-    handle = current_stream_handle(q.device) if stream is None else stream
-    if counters is COUNTERS_DEFAULT:
-        counters = None
-        if split_k > 1:
-            q_len = q.shape[1] if q.dim() == 4 else 1
-            counters = stream_counters(q.device, handle, decode_ticket_count(q.shape[0], q.shape[-2], q_len))
+    ``[B, T, H, D]`` (multi-token decode, ``q_len = T``)."""
     a = decode_args(q, k_cache, v_cache, page_table, seq_lens, out, page_size, softmax_scale, split_k,
                     workspace=workspace, k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group,
-                    pages_per_split=pages_per_split, kernel=kernel, counters=counters)
+                    pages_per_split=pages_per_split, kernel=kernel)
+    handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
 
 
@@ -446,15 +398,8 @@ def decode_args(
     waves_per_group: int = 0,
     pages_per_split: int = 0,
     kernel: int = KERNEL_AUTO,
-    counters: torch.Tensor | None = None,
 ) -> DecodeArgs:
-    """The ``fat_decode_args`` block of a decode launch (see paged_decode;
-    ``counters``: zeroed int32 split-K ticket counters, or None)."""
-    if counters is not None:
-        q_len = q.shape[1] if q.dim() == 4 else 1
-        need = decode_ticket_count(q.shape[0], q.shape[-2], q_len)
-        if counters.dtype != torch.int32 or counters.device != q.device or counters.numel() < need:
-            raise ValueError(f"counters must be int32 on {q.device} with at least {need} elements")
+    """The ``fat_decode_args`` block of a decode launch (see paged_decode)."""
     multi = q.dim() == 4
     a = DecodeArgs()
     a.q = _ptr(q)
@@ -492,7 +437,6 @@ def decode_args(
     a.pages_per_split = int(pages_per_split)
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
-    a.split_counters = _ptr(counters)
     return a
 
 

@@ -437,11 +437,6 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
       }
     }
   }
-  if (S > 1 && p.ctr)
-    merge_partitions_if_last<QT>(p, b, S, D, nvalid, [&](int rr, int& t, int& h) {
-      t = 0;
-      h = head0 + rr;
-    });
 }
 
 // ---------------------------------------------------------------------------
@@ -762,12 +757,6 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
       }
     }
   }
-  if (S > 1 && p.ctr)
-    merge_partitions_if_last<QT>(p, b, S, D, nvalid, [&](int r, int& t, int& h) {
-      const int rr = row_base + r;
-      t = rr / p.group;
-      h = kvh * p.group + (rr - t * p.group);
-    });
 }
 
 // Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
@@ -1067,7 +1056,6 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   const size_t acc_elems = (size_t)a->batch * T * a->num_heads * a->split_k * D;
   prm.ws_acc = a->split_k > 1 ? static_cast<float*>(a->workspace) : nullptr;
   prm.ws_ml = a->split_k > 1 ? static_cast<float*>(a->workspace) + acc_elems : nullptr;
-  prm.ctr = a->split_k > 1 ? a->split_counters : nullptr;
   prm.q_sb = a->q_stride_b;
   prm.q_sh = a->q_stride_h;
   prm.q_st = T > 1 ? a->q_stride_t : 0;
@@ -1102,7 +1090,7 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
       a->pages_per_split > 0 ? a->pages_per_split : ((int64_t)a->max_pages + a->split_k - 1) / a->split_k;
   if (generic) {
     const int rc = fat_host::launch_decode_generic(prm, a->q_dtype, kv, D, HG, grid, stream);
-    if (rc != FAT_OK || a->split_k == 1 || prm.ctr) return rc;
+    if (rc != FAT_OK || a->split_k == 1) return rc;
     return launch_merge(prm, a, D, stream);
   }
   if (use_mfma) {
@@ -1114,7 +1102,7 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, nw, grid, stream);
     else launch_decode_mfma_q<fat::BF16>(prm, kv, D, nw, grid, stream);
     const int rc = fat_host::launch_status("paged_decode_mfma_kernel");
-    if (rc != FAT_OK || a->split_k == 1 || prm.ctr) return rc;
+    if (rc != FAT_OK || a->split_k == 1) return rc;
     return launch_merge(prm, a, D, stream);
   }
   // 8-wave workgroups keep more loads in flight per CU.  They pay off when
@@ -1126,7 +1114,7 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
                                     : ((wgs < 2 * 256 || pages_per_wg * a->page_size >= 1024) ? 8 : 4);
   int rc = (a->q_dtype == FAT_DTYPE_F16) ? launch_decode_q<fat::F16>(prm, kv, D, HG, nw, grid, stream)
                                          : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);
-  if (rc != FAT_OK || a->split_k == 1 || prm.ctr) return rc;
+  if (rc != FAT_OK || a->split_k == 1) return rc;
 
   return launch_merge(prm, a, D, stream);
 }
@@ -1137,17 +1125,13 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
 // own copy of `scratch` (kScratchBytes) until the process ends.  Its device
 // address is looked up once per device with hipGetSymbolAddress (the array's
 // name is only a host-side stand-in) and used for every launch after that.
-// Layout: the partials region (FAT_DECODE_NOALLOC_MAX_WORKSPACE bytes), then
-// FAT_DECODE_NOALLOC_MAX_TICKETS split-K ticket counters.  The partials need
-// no clearing (each partition of a launch writes its whole (acc, m, l) row
-// before anything reads it); the counters are zero from load (the array has
-// no initialiser) and every completed launch leaves them zero.  Two calls
-// that overlap on one GPU (different streams) share the array and race.
+// Nothing in it needs clearing: each partition of a launch writes its whole
+// (acc, m, l) row before the merge reads it.  Two calls that overlap on one
+// GPU (different streams) share the array and race.
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr size_t kScratchPartials = FAT_DECODE_NOALLOC_MAX_WORKSPACE;
-constexpr size_t kScratchBytes = kScratchPartials + (size_t)FAT_DECODE_NOALLOC_MAX_TICKETS * sizeof(int32_t);
+constexpr size_t kScratchBytes = FAT_DECODE_NOALLOC_MAX_WORKSPACE;
 constexpr int kMaxDevices = 64;
 
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
@@ -1185,18 +1169,14 @@ extern "C" int fat_paged_decode_noalloc(const fat_decode_args* a, void* stream) 
   const int64_t rows = (int64_t)a->batch * (a->q_len > 1 ? a->q_len : 1);
   const size_t need = a->split_k > 1 ? (size_t)rows * a->num_heads * a->split_k * (a->head_dim + 2) * sizeof(float)
                                      : 0;
-  if (need > kScratchPartials) {
+  if (need > kScratchBytes) {
     fat_host::set_error("fat_paged_decode_noalloc: this launch needs %zu bytes of split-K workspace; the "
                         "allocation-free entry holds at most %zu (lower split_k, or use fat_paged_decode with a "
-                        "workspace)", need, kScratchPartials);
+                        "workspace)", need, kScratchBytes);
     return FAT_E_INVALID;
   }
   fat_decode_args b = *a;
   b.workspace = need ? g_scratch_ptr[dev] : nullptr;
-  const bool tickets = need && rows * a->num_heads <= FAT_DECODE_NOALLOC_MAX_TICKETS;
-  b.split_counters = tickets ? reinterpret_cast<int32_t*>(static_cast<uint8_t*>(g_scratch_ptr[dev]) +
-                                                          kScratchPartials)
-                             : nullptr;
   const int rc = fat_paged_decode(&b, stream);
   if (rc != FAT_OK) {
     // Name this entry in the message the shared path set.

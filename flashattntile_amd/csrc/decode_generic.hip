@@ -247,11 +247,6 @@ __global__ __launch_bounds__(256) void paged_decode_generic_kernel(const DecodeP
       }
     }
   }
-  if (S > 1 && p.ctr)
-    merge_partitions_if_last<QT>(p, b, S, D, nvalid, [&](int r, int& t, int& h) {
-      t = 0;
-      h = head0 + r;
-    });
 }
 
 }  // namespace fat

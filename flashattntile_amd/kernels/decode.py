@@ -371,8 +371,7 @@ class DecodeLaunch:
     and ``out`` passed to :meth:`run` must have the dtype, shape and strides
     of the ``q`` given here (``out``: contiguous).  ``q`` is ``[B, H, D]`` or
     ``[B, T, H, D]`` (multi-token decode); ``scales`` selects an int8 /
-    float8_e4m3fn cache.  A plan runs one launch at a time: its split-K
-    workspace and ticket counters are its own.
+    float8_e4m3fn cache.
     """
 
     def __init__(self, q: torch.Tensor, cache: PagedKVCache, softmax_scale: float | None = None,
@@ -414,15 +413,6 @@ class DecodeLaunch:
         rows = q.shape[0] * q_len
         need = _hip.decode_workspace_bytes(rows, q.shape[-2], q.shape[-1], cfg["split_k"])
         self.workspace = torch.empty(max(1, need), dtype=torch.uint8, device=q.device) if need else None
-        # Split-K tickets of this plan (the partitions merge inside the launch;
-        # every completed run leaves them zero).  Not inside a graph capture,
-        # where the zero fill would be a captured allocation: the launch then
-        # merges with a second kernel.
-        self.counters = None
-        if need and not torch.cuda.is_current_stream_capturing():
-            self.counters = torch.zeros(_hip.decode_ticket_count(q.shape[0], q.shape[-2], q_len), dtype=torch.int32,
-                                        device=q.device)
-            torch.cuda.current_stream(q.device).synchronize()
         self._keep = (cache, k_scale, v_scale)  # the argument block points into these
         self._shape, self._dtype = tuple(q.shape), q.dtype
         self._device = q.device
@@ -430,8 +420,7 @@ class DecodeLaunch:
                                       cache.page_size, self.softmax_scale, cfg["split_k"],
                                       workspace=self.workspace, k_scale=k_scale, v_scale=v_scale,
                                       waves_per_group=cfg["num_warps"] or 0,
-                                      pages_per_split=cfg["pages_per_split"], kernel=_KERNEL_CODES[cfg["kernel"]],
-                                      counters=self.counters)
+                                      pages_per_split=cfg["pages_per_split"], kernel=_KERNEL_CODES[cfg["kernel"]])
 
     def run(self, q: torch.Tensor, out: torch.Tensor | None = None, stream: int | None = None) -> torch.Tensor:
         """Decode ``q`` into ``out`` (default: a new tensor) on ``stream``

@@ -43,16 +43,13 @@
 extern "C" {
 #endif
 
-/* 11: fat_decode_args.split_counters: split-K partitions merged inside the
- *     decode launch (no second kernel) when the caller passes ticket
- *     counters.
- * 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
+/* 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
  *     uses the workspace for an fp16 copy of V (optional).
  * 9: fat_paged_decode_noalloc (allocation-free decode).
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 11
+#define FAT_ABI_VERSION 10
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -129,8 +126,7 @@ enum fat_status {
  * split_k * pages_per_split).  With split_k > 1 the partitions are merged by
  * a log-sum-exp reduction through `workspace`, which must hold
  * fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k) bytes
- * (it may be NULL when split_k == 1): inside the decode launch when
- * `split_counters` is given, else by a second kernel.  int8/fp8 pages: with bf16 queries
+ * (it may be NULL when split_k == 1).  int8/fp8 pages: with bf16 queries
  * K and V are dequantised as round_to_bf16(float(x) * scale), as
  * dequantize_kv_pages (flashattn_tile/quant.py:145-161) followed by the fp32
  * reference does.  With fp16 queries k_scale multiplies the fp32 scores of
@@ -178,15 +174,6 @@ typedef struct fat_decode_args {
   int64_t q_stride_t, out_stride_t;
   int32_t q_len;
   int32_t kernel; /* FAT_KERNEL_AUTO, _DECODE_VALU, _MFMA or _GENERIC */
-  /* Split-K merge inside the decode launch (split_k > 1): NULL, or at least
-   * batch * max(q_len, 1) * num_heads int32 ticket counters that are all 0.
-   * With counters, the last partition workgroup of each (sequence, query
-   * head group) to finish merges the partitions from `workspace` and sets
-   * its counter back to 0, so every completed launch leaves them 0 again
-   * (graph replays included); without them a second kernel merges.  Zero
-   * them once when allocating (a fill kernel, e.g. torch.zeros).  Launches
-   * that may overlap (two streams) need counters of their own. */
-  int32_t* split_counters;
 } fat_decode_args;
 
 /*
@@ -375,13 +362,8 @@ int fat_paged_decode(const fat_decode_args* args, void* stream);
  * (fat_paged_decode_workspace_bytes of its batch * q_len rows) exceeds the
  * maximum returns FAT_E_INVALID.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (e.g. on two streams) race.  The
- * current HIP device must be the one `stream` belongs to.  args->
- * split_counters is ignored too: the array also holds
- * FAT_DECODE_NOALLOC_MAX_TICKETS ticket counters (zero from load), used
- * when batch * max(q_len, 1) * num_heads fits in them (else the partitions
- * are merged by a second kernel). */
+ * current HIP device must be the one `stream` belongs to. */
 #define FAT_DECODE_NOALLOC_MAX_WORKSPACE ((size_t)32 << 20)
-#define FAT_DECODE_NOALLOC_MAX_TICKETS 16384
 int fat_paged_decode_noalloc(const fat_decode_args* args, void* stream);
 
 /* Bytes of the optional fat_prefill_varlen workspace (used by bf16). */
