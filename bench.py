@@ -36,8 +36,10 @@ import time
 
 import torch
 
-HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = 2516.6  # dense fp16 / bf16
+from flashattntile_amd.env import peak_hbm_gbs, peak_mfma_tflops  # noqa: E402
+
+HBM_PEAK_GBS = peak_hbm_gbs()
+MFMA_PEAK_TFLOPS = peak_mfma_tflops("fp16")  # dense fp16 / bf16
 MALL_BYTES = 256 << 20
 FLUSH_BYTES = 512 << 20
 
@@ -62,26 +64,27 @@ def _parse():
     ap.add_argument("--report", default="", help="with --all-configs: write the table to this JSON file")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle timing per sample")
     ap.add_argument("--only", default="", help="with --all-configs: run only rows whose name contains this text")
+    ap.add_argument("--source-digests", action="store_true",
+                    help="print the kernel-source digests that profiles/traffic.json entries are stamped with, "
+                         "and exit")
     return ap.parse_args()
 
 
-def _cores() -> int:
-    try:
-        n = len(os.sched_getaffinity(0))
-    except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))  # the GPU box's CPU share is 16 cores
+def _host() -> dict:
+    """Affinity core count, os.cpu_count(), cgroup CPU quota and the full CPU
+    model of this host (flashattntile_amd.env.host_info)."""
+    from flashattntile_amd.env import host_info
+
+    return host_info()
 
 
-def _cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+def _cores(info: dict | None = None) -> int:
+    """Threads for the CPU baselines: every core this process may run on,
+    bounded only by a cgroup CPU quota when one is set (more threads than the
+    quota only time-slice)."""
+    from flashattntile_amd.env import cpu_threads
+
+    return cpu_threads(info or _host())
 
 
 def copy_calibration(device, nbytes=1 << 30):
@@ -317,7 +320,8 @@ def bench_prefill(args, device, seq=8192):
                          "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"],
                          "traffic": (_traffic_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128")
                                      if name == "f16" else None),
-                         "mfma_busy": _mfma_busy_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128", name)},
+                         "mfma_busy": _mfma_busy_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128", name),
+                         "counters_source": _profile_entry(f"prefill_causal_seq{seq}_h32_kv8_d128")[1]},
         }
     res["workload"] = f"prefill_causal_seq{seq}_h32_kv8_d128"
     res["steps"] = steps
@@ -327,11 +331,14 @@ def bench_prefill(args, device, seq=8192):
 def cpu_baseline_decode(budget_s=12.0):
     """fp32 oracle (oracle/reference.py) on a bounded sample of the decode
     workload: 4 of the 32 sequences (ctx 4096, 32/8 heads, D128, fp16 pages
-    upcast), timed with perf_counter, min over repetitions within ~budget_s."""
+    upcast), timed with perf_counter, min over repetitions within ~budget_s.
+    Records the threads used, the affinity core count, os.cpu_count(), the
+    cgroup CPU quota and the CPU model."""
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
-    cores = _cores()
+    host = _host()
+    cores = _cores(host)
     torch.set_num_threads(cores)
     B, CTX, HQ, HKV, D, P = 4, 4096, 32, 8, 128, 16
     q, pools, _, _, table, lens = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device="cpu")
@@ -344,7 +351,8 @@ def cpu_baseline_decode(budget_s=12.0):
         "cores": cores,
         "kind": "port",
         "sample": f"fp32 oracle ref_attention_paged on 4 of the 32 sequences (ctx 4096, 32/8 heads, D128, "
-                  f"page 16, fp16 pages upcast); min of {reps} runs after 1 warm-up; {_cpu_model()}",
+                  f"page 16, fp16 pages upcast); min of {reps} runs after 1 warm-up; {cores} torch threads",
+        "host": host,
         "ms": best * 1e3,
     }
 
@@ -415,6 +423,53 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
             "timing": timing,
             "cpu": {"value": round(cpu_bytes / best / 1e9, 3), "unit": "GB/s",
                     "sample": f"{nb} of {len(lens)} sequences, min of {reps}"}}
+
+
+def _configs0_row(device, args, flush):
+    """BASELINE configs[0], the reference's CPU workload: B4, 32/8 heads, D128,
+    page 16, ctx ~ U{64..512} (seeded), a 256-page pool and a seeded
+    randperm(256) table sliced to [4, 32], fp16 pages.  The GPU decode (the
+    product's launch for the shape) and the fp32 oracle over the whole batch
+    (min of 21 runs after 3 warm-ups, the reference's CPU convention)."""
+    name = "decode fp16 configs[0] B4 ctx U[64,512] pool256"
+    if args.only and args.only not in name:
+        return None
+    from flashattntile_amd import _hip
+    from flashattntile_amd.autotune import bytes_decode_paged
+    from oracle.reference import ref_attention_paged
+
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(64, 513, (4,), generator=g).to(torch.int32)
+    table = torch.randperm(256, generator=g)[:128].to(torch.int32).view(4, 32)
+    k = torch.randn(256, 16, 8, 128, generator=g).half()
+    v = torch.randn(256, 16, 8, 128, generator=g).half()
+    q = torch.randn(4, 32, 128, generator=g).half()
+    kd, vd, qd = k.to(device), v.to(device), q.to(device)
+    td, ld = table.to(device), lens.to(device)
+    pools = [(kd, vd, None, None)]
+    sk, pps, waves, kern, source = _product_launch(qd, pools, td, ld, 16, int(lens.max()), 256)
+    out = torch.empty_like(qd)
+    ws = torch.empty(max(1, _hip.decode_workspace_bytes(4, 32, 128, sk)), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device)
+    handle = int(stream.cuda_stream)
+
+    def step(i):
+        _hip.paged_decode(qd, kd, vd, td, ld, out, 16, 128 ** -0.5, sk, workspace=ws, stream=handle,
+                          pages_per_split=pps, waves_per_group=waves, kernel=kern)
+
+    ms = _time_steps_flushed(step, max(20, args.steps // 4), 5, stream, flush)
+    nbytes = bytes_decode_paged(lens.tolist(), 32, 8, 128)
+    for _ in range(2):
+        ref_attention_paged(q, k, v, table, lens)
+    best, reps = _time_cpu(lambda: ref_attention_paged(q, k, v, table, lens), args.cpu_budget, max_reps=21)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"config": name, "kind": "decode", "value": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "us": round(ms * 1e3, 2), "bytes": nbytes, "split_k": sk,
+            "pages_per_split": pps, "launch": {"waves": waves, "kernel": kern, "source": source},
+            "lens": lens.tolist(),
+            "timing": "median of per-launch events, each after a 512 MB cache flush",
+            "cpu": {"value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "us": round(best * 1e6, 1),
+                    "sample": f"the whole configs[0] batch, min of {reps} after 3 warm-ups, {_cores()} threads"}}
 
 
 def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
@@ -716,6 +771,8 @@ def all_configs(args, device):
         print(f"# {row['config']:46s} {row['value']:9.1f} {row['unit']:8s} ({100 * row['frac']:5.1f}% of peak, "
               f"{row['us']:9.1f} us)  {tail}", file=sys.stderr, flush=True)
 
+    # the reference's CPU workload, GPU decode next to the fp32 oracle
+    emit(_configs0_row(device, args, flush))
     # fp16 decode sweep (and bf16 at the headline shape)
     for B in (1, 8, 32, 128):
         for ctx in (128, 1024, 4096, 16384):
@@ -767,28 +824,68 @@ def all_configs(args, device):
     return rows
 
 
-def _profile_entry(workload: str) -> dict:
-    """The rocprofv3 PMC measurements of a workload (profiles/traffic.json)."""
+# Kernel sources behind each profiled workload.  A profiles/traffic.json
+# entry records the digest of these files at the commit its rocprofv3 PMC
+# passes ran on; the bench line carries its figures only while the files
+# still hash to that digest (otherwise the kernel changed since).
+PROFILE_SOURCES = {
+    "decode": ["flashattntile_amd/csrc/decode.hip", "flashattntile_amd/csrc/decode_params.h",
+               "flashattntile_amd/csrc/fat_common.h"],
+    "prefill": ["flashattntile_amd/csrc/prefill.hip", "flashattntile_amd/csrc/fat_common.h"],
+    "kvwrite": ["flashattntile_amd/csrc/kvwrite.hip", "flashattntile_amd/csrc/fat_common.h"],
+}
+
+
+def source_digest(family: str) -> str:
+    """sha256 (first 16 hex digits) over the path and bytes of each source
+    file of a kernel family, in PROFILE_SOURCES order."""
+    import hashlib
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    h = hashlib.sha256()
+    for rel in PROFILE_SOURCES[family]:
+        h.update(rel.encode())
+        with open(os.path.join(root, rel), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def _profile_entry(workload: str) -> tuple[dict, str]:
+    """The rocprofv3 PMC measurements of a workload (profiles/traffic.json)
+    and where they come from; ({}, reason) when absent or measured on other
+    kernel sources than this tree's."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as fh:
-            return json.load(fh).get(workload, {})
+            entry = json.load(fh).get(workload, {})
     except (OSError, ValueError):
-        return {}
+        return {}, "profiles/traffic.json unreadable"
+    if not entry:
+        return {}, f"no PMC entry for {workload}"
+    family = entry.get("family")
+    if family not in PROFILE_SOURCES or entry.get("source_digest") != source_digest(family):
+        return {}, (f"stale: {workload}'s PMC passes ran on kernel sources with digest "
+                    f"{entry.get('source_digest')}, this tree's are {source_digest(family) if family in PROFILE_SOURCES else '?'}")
+    return entry, entry.get("source", "profiles/traffic.json")
 
 
 def _traffic_from_profiles(workload: str):
-    """HBM bytes per launch measured by rocprofv3 PMC runs."""
-    return _profile_entry(workload).get("bytes_per_launch")
+    """HBM bytes per launch measured by rocprofv3 PMC runs on this tree's
+    kernel sources (None when stale or absent)."""
+    return _profile_entry(workload)[0].get("bytes_per_launch")
 
 
 def _mfma_busy_from_profiles(workload: str, dtype: str):
-    """Fraction of the kernel's cycles the MFMA pipe was busy (PMC run)."""
-    return _profile_entry(workload).get("mfma_busy", {}).get(dtype)
+    """Fraction of the kernel's cycles the MFMA pipe was busy (PMC run on
+    this tree's kernel sources; None when stale or absent)."""
+    return _profile_entry(workload)[0].get("mfma_busy", {}).get(dtype)
 
 
 def main():
     args = _parse()
+    if args.source_digests:
+        print(json.dumps({f: source_digest(f) for f in PROFILE_SOURCES}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); every MI355X box here has "
               "one GPU and the attention path needs no collectives.  Run with --gpus 1.", file=sys.stderr)
@@ -807,7 +904,7 @@ def main():
 
     if args.all_configs:
         rows = all_configs(args, device)
-        report = {"cores": _cores(), "cpu_model": _cpu_model(), "rows": rows,
+        report = {"cores": _cores(), "host": _host(), "rows": rows,
                   "device": torch.cuda.get_device_name(device)}
         if args.report:
             with open(args.report, "w") as fh:
@@ -870,6 +967,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": _traffic_from_profiles(workload),
+            "traffic_source": _profile_entry(workload)[1],
             "algorithmic_bytes": dec["bytes"],
         },
         "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "ms"},

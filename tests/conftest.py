@@ -32,3 +32,21 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Worst parity figures of the run per output dtype (tests/_parity.py)."""
+    try:
+        from _parity import RECORDS
+    except ImportError:  # pragma: no cover
+        return
+    if not RECORDS:
+        return
+    terminalreporter.write_sep("-", "parity against the fp32 oracle (worst per output dtype)")
+    for dt in sorted({r[1] for r in RECORDS}):
+        rows = [r for r in RECORDS if r[1] == dt]
+        raw = max(rows, key=lambda r: r[2])
+        fp = max(rows, key=lambda r: r[3])
+        terminalreporter.write_line(
+            f"{dt}: {len(rows)} checks; max |out - oracle({dt})| = {raw[2]:.3e} ({raw[0]}); "
+            f"max |out - oracle(fp32)| = {fp[3]:.3e} ({fp[0]})")
