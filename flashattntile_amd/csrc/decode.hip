@@ -8,10 +8,10 @@
 //   * one workgroup per (split, GQA head group, sequence); the HG query heads
 //     of a group share one KV head, so every K/V page is read from HBM once
 //     per group instead of once per query head;
-//   * a wave streams 16-token units; lane (r, c) owns row r of each 16-byte
-//     wide load and dims [c*EPL, c*EPL+EPL); K and V rows arrive as
-//     global_load_dwordx4, one unit ahead of the compute (register double
-//     buffer);
+//   * a wave streams 16-token units (32 at fp16/bf16 head_dim 64); lane
+//     (r, c) owns row r of each 16-byte wide load and dims
+//     [c*EPL, c*EPL+EPL); K and V rows arrive as global_load_dwordx4, one
+//     unit ahead of the compute (register double buffer);
 //   * q.k partial sums are reduced across the LPR lanes of a row with a
 //     transposing DPP butterfly that leaves one (head, token) score per lane;
 //   * softmax state (running max m, sum l) is shared by the whole wave; the
@@ -63,7 +63,13 @@ struct Geom {
   static constexpr int kEpl = 16 / kElemBytes;  // elements per lane per row
   static constexpr int kLpr = D / kEpl;         // lanes per row
   static constexpr int kRpl = 64 / kLpr;        // rows per load
-  static constexpr int kNi = 16 / kRpl;         // loads per 16-token unit
+  static constexpr int kNi16 = 16 / kRpl;       // loads per 16 tokens
+  // Tokens per streamed unit: 16, or 32 when 16 tokens take only two loads
+  // per lane for each of K and V (fp16/bf16 at head_dim 64), so a wave keeps
+  // as many bytes in flight as at head_dim 128.
+  static constexpr int kUnit = (KV == KV_SAME && kNi16 == 2) ? 32 : 16;
+  static constexpr int kUnitLog2 = kUnit == 32 ? 5 : 4;
+  static constexpr int kNi = kUnit / kRpl;      // loads per unit
   static_assert(kLpr == 4 || kLpr == 8 || kLpr == 16, "unsupported head_dim / element size");
 };
 
@@ -169,7 +175,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   const int pe = split == S - 1 ? np : min(np, pb + pps);
   const int t_begin = pb << p.log2P;
   const int t_end = min(seq_len, pe << p.log2P);
-  const int n_units = t_end > t_begin ? (t_end - t_begin + 15) >> 4 : 0;
+  constexpr int UL = Gm::kUnitLog2;
+  const int n_units = t_end > t_begin ? (t_end - t_begin + Gm::kUnit - 1) >> UL : 0;
 
   // q for the HG heads, packed pairs of QT (padded heads reuse head0).
   u32 qv[HG][QW];
@@ -193,7 +200,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   constexpr int EB = Gm::kElemBytes;
 
   auto fetch = [&](UnitRegs<NI>& R, int u) {
-    const int base = t_begin + (u << 4);
+    const int base = t_begin + (u << UL);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       int rs = base + i * RPL;
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   for (int u = w; u < n_units; u += NW) {
     const UnitRegs<NI> cur = nxt;
     if (u + NW < n_units) fetch(nxt, u + NW);
-    const int base = t_begin + (u << 4);
+    const int base = t_begin + (u << UL);
 
     // ---- scores: partial q.k over this lane's EPL dims ----
     float part[NV];
