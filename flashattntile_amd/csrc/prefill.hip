@@ -287,8 +287,11 @@ constexpr float kLazy = 8.0f;
 // rows (group g tiles g, g + 2, ...) and merge (m, l, O) through LDS at the
 // end, halving the tile chain of a query block: for grids too small to
 // give every CU more than one workgroup.
+// D = 256 (NG = 1 only) holds O (128 registers) and Q (64) per lane and runs
+// one wave per SIMD with up to 512 registers.
 template <typename T, int D, bool CAUSAL, bool POS, int PG, int NG>
-__global__ __launch_bounds__(256 * NG) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256 * NG)
+__attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, D >= 256 ? 1 : 2)))
 void prefill_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;        // MFMA k-steps of S^T over the head dim
   constexpr int DB = D / 32;        // 32-row blocks of O^T
@@ -1209,26 +1212,44 @@ size_t vpre_bytes_v16(int64_t total_k, int64_t hkv, int64_t d) {
 template <typename T, int D, int PG>
 int launch_prefill_t(const fat::PrefillParams& prm, bool causal, PrefillKind kind, dim3 grid, hipStream_t stream) {
   const bool pos = prm.scale_log2 > 0.f;
-  if (kind == PF_PINGPONG) {
-    if constexpr (std::is_same<T, fat::BF16>::value && PG == 0) {
-      if (prm.v_head_scale) {
-        if (causal) launch_prefill_pp_c<T, D, true, PG, true>(prm, pos, grid, stream);
-        else launch_prefill_pp_c<T, D, false, PG, true>(prm, pos, grid, stream);
-        return fat_host::launch_status("prefill_pp_kernel");
-      }
-    }
-    if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
-    else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
-    return fat_host::launch_status("prefill_pp_kernel");
-  }
-  if (kind == PF_4WAVE_SPLIT) {
-    if (causal) launch_prefill_c<T, D, true, PG, 2>(prm, pos, grid, stream);
-    else launch_prefill_c<T, D, false, PG, 2>(prm, pos, grid, stream);
-  } else {
+  if constexpr (D == 256) {  // the 4-wave kernel only (launch_prefill checked kind)
+    (void)kind;
     if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, pos, grid, stream);
     else launch_prefill_c<T, D, false, PG, 1>(prm, pos, grid, stream);
+    return fat_host::launch_status("prefill_kernel");
+  } else {
+    if (kind == PF_PINGPONG) {
+      if constexpr (std::is_same<T, fat::BF16>::value && PG == 0) {
+        if (prm.v_head_scale) {
+          if (causal) launch_prefill_pp_c<T, D, true, PG, true>(prm, pos, grid, stream);
+          else launch_prefill_pp_c<T, D, false, PG, true>(prm, pos, grid, stream);
+          return fat_host::launch_status("prefill_pp_kernel");
+        }
+      }
+      if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
+      else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
+      return fat_host::launch_status("prefill_pp_kernel");
+    }
+    if (kind == PF_4WAVE_SPLIT) {
+      if (causal) launch_prefill_c<T, D, true, PG, 2>(prm, pos, grid, stream);
+      else launch_prefill_c<T, D, false, PG, 2>(prm, pos, grid, stream);
+    } else {
+      if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, pos, grid, stream);
+      else launch_prefill_c<T, D, false, PG, 1>(prm, pos, grid, stream);
+    }
+    return fat_host::launch_status("prefill_kernel");
   }
-  return fat_host::launch_status("prefill_kernel");
+}
+
+template <typename T, int PG>
+int launch_prefill_d(const fat::PrefillParams& prm, int D, bool causal, PrefillKind kind, dim3 grid,
+                     hipStream_t stream) {
+  switch (D) {
+    case 128: return launch_prefill_t<T, 128, PG>(prm, causal, kind, grid, stream);
+    case 64: return launch_prefill_t<T, 64, PG>(prm, causal, kind, grid, stream);
+    case 32: return launch_prefill_t<T, 32, PG>(prm, causal, kind, grid, stream);
+    default: return launch_prefill_t<T, 256, PG>(prm, causal, kind, grid, stream);  // 256 (checked)
+  }
 }
 
 bool valid_prefill_kernel(int kernel) {
@@ -1269,6 +1290,16 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
            : kernel == FAT_KERNEL_PREFILL_4WAVE  ? PF_4WAVE
                                                  : PF_4WAVE_SPLIT;
   }
+  // head_dim 256: O and Q alone take 192 registers per lane, so only the
+  // 4-wave kernel (one wave per SIMD) runs it; its K/V tiles take 141 KB of
+  // LDS, which leaves no room for the split's second group.
+  if (D == 256) {
+    if (kernel != FAT_KERNEL_AUTO && kind != PF_4WAVE) {
+      fat_host::set_error("%s: head_dim 256 runs on the 4-wave prefill kernel only (kernel %d)", who, kernel);
+      return FAT_E_UNSUPPORTED;
+    }
+    kind = PF_4WAVE;
+  }
   const int bm = kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
   prm.nqb = (max_seqlen_q + bm - 1) / bm;
   prm.scale_log2 = softmax_scale * fat::kLog2e;
@@ -1296,10 +1327,15 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
                          total_k, nblk, blockmax);
       hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<128>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
                          total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
-    } else {
+    } else if (D == 64) {
       hipLaunchKernelGGL((fat::bf16v_expmax_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
                          total_k, nblk, blockmax);
       hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+    } else {
+      hipLaunchKernelGGL((fat::bf16v_expmax_kernel<32>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
+                         total_k, nblk, blockmax);
+      hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<32>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
                          total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
     }
     const int rc = fat_host::launch_status("bf16v_to_f16_kernel");
@@ -1309,12 +1345,8 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     prm.v_sh = D;
     prm.v_head_scale = head_scale;
   }
-  if (dtype == FAT_DTYPE_F16) {
-    return D == 128 ? launch_prefill_t<fat::F16, 128, PG>(prm, causal, kind, grid, stream)
-                    : launch_prefill_t<fat::F16, 64, PG>(prm, causal, kind, grid, stream);
-  }
-  return D == 128 ? launch_prefill_t<fat::BF16, 128, PG>(prm, causal, kind, grid, stream)
-                  : launch_prefill_t<fat::BF16, 64, PG>(prm, causal, kind, grid, stream);
+  if (dtype == FAT_DTYPE_F16) return launch_prefill_d<fat::F16, PG>(prm, D, causal, kind, grid, stream);
+  return launch_prefill_d<fat::BF16, PG>(prm, D, causal, kind, grid, stream);
 }
 
 }  // namespace
@@ -1354,8 +1386,8 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 64 && D != 128) {
-    fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (64 or 128)", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (32, 64, 128 or 256)", D);
     return FAT_E_UNSUPPORTED;
   }
   if (a->max_seqlen_q < 0 || a->max_seqlen_k < 0) {
@@ -1439,8 +1471,8 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 64 && D != 128) {
-    fat_host::set_error("fat_prefill_paged: head_dim %d unsupported (64 or 128)", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    fat_host::set_error("fat_prefill_paged: head_dim %d unsupported (32, 64, 128 or 256)", D);
     return FAT_E_UNSUPPORTED;
   }
   const int P = a->page_size;

@@ -183,6 +183,9 @@ typedef struct fat_decode_args {
  *   cu_seqlens_q / cu_seqlens_k int32 [batch + 1], starting at 0,
  *   non-decreasing, kv_len >= q_len per sequence when causal.
  *   out [total_q, num_heads, head_dim]      dtype
+ * head_dim is 32, 64, 128 or 256; 256 runs on the 4-wave kernel only
+ * (FAT_KERNEL_AUTO or FAT_KERNEL_PREFILL_4WAVE; the others return
+ * FAT_E_UNSUPPORTED).  The same holds for fat_prefill_paged.
  * Causal masking is bottom-right aligned: query i of a sequence sees key j
  * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
  * `workspace` is optional (NULL, or 256-byte aligned and holding

@@ -51,6 +51,36 @@ def test_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
     assert_parity(out, _ref32(q, k, v, cu, cu, causal), label=label)
 
 
+# head_dim 32 runs on every prefill kernel; head_dim 256 on the 4-wave kernel
+# only (O and Q take 192 registers per lane), which the others refuse.
+HEAD_DIM_KERNELS = {32: [None, "pingpong", "4wave", "4wave_split"], 256: [None, "4wave"]}
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d", [32, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_head_dims_32_and_256(dtype, d, causal):
+    """The reference's prefill is generic over a power-of-two head_dim
+    (flashattn_tile/kernels/prefill.py:59-89); 32 and 256 against the oracle
+    on ragged lengths, GQA 8/2, every kernel that takes them."""
+    q, k, v, cu = make_varlen(ODD_LENS, 8, 2, d, dtype, seed=d + 3, device=DEV)
+    ref = _ref32(q, k, v, cu, cu, causal)
+    for kern in HEAD_DIM_KERNELS[d]:
+        label = f"prefill {kern or 'auto'} {dtype} D{d} causal={causal}"
+        print(label, flush=True)
+        out = prefill_attention(q, k, v, cu, cu, max(ODD_LENS), max(ODD_LENS), causal=causal,
+                                config={"kernel": kern})
+        torch.cuda.synchronize()
+        assert_parity(out, ref, label=label)
+
+
+def test_prefill_head_dim_256_refuses_the_8_wave_kernels():
+    q, k, v, cu = make_varlen([70], 4, 2, 256, torch.float16, seed=4, device=DEV)
+    for kern in ("pingpong", "4wave_split"):
+        with pytest.raises(RuntimeError, match="head_dim 256 runs on the 4-wave"):
+            prefill_attention(q, k, v, cu, cu, 70, 70, causal=True, config={"kernel": kern})
+
+
 @pytest.mark.parametrize("seqlen", [1, 2, 63, 64, 65, 127, 128, 129, 1000])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_prefill_single_odd_length(seqlen, dtype, kernel):

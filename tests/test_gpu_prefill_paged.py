@@ -66,6 +66,23 @@ def test_paged_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
     assert_parity(out, _ref32(q, cache, cu, causal), label=label)
 
 
+@pytest.mark.parametrize("P", [4, 16, 64])
+@pytest.mark.parametrize("d", [32, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_prefill_head_dims_32_and_256(dtype, d, P):
+    """head_dim 32 and 256 through the page table, with pages below, at and
+    above the rows of one 16-byte-per-lane load (64 at D32, 8 at D256), on
+    the library's kernel choice."""
+    label = f"paged prefill {dtype} D{d} P{P}"
+    print(label, flush=True)
+    lens_k = [c[0] for c in CHUNKS]
+    lens_q = [c[1] for c in CHUNKS]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, d, P, dtype, seed=d + P)
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache, cu, True), label=label)
+
+
 @pytest.mark.parametrize("P", [1, 4, 16, 32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_paged_prefill_page_sizes(P, dtype, kernel):
