@@ -193,7 +193,9 @@ typedef struct fat_decode_args {
  * fp16 ignores it.  With bf16 the large-grid kernel then stages an fp16
  * copy of V written there by a pre-pass (one power-of-two scale per KV
  * head; results within the same bound as the in-kernel conversion it
- * replaces); without it the kernel converts V tile by tile.
+ * replaces) when the sequences average at least 2048 query tokens, where
+ * the copy costs less than it saves; otherwise, or without the workspace,
+ * the kernel converts V tile by tile.
  */
 typedef struct fat_prefill_args {
   const void* q;

@@ -173,15 +173,15 @@ def test_prefill_bf16_v_beyond_fp16_range(huge, kernel):
     """bf16 V rows of magnitude >= 2^15: V is staged as fp16 scaled by 2^-s
     (per staging wave in the 4-wave kernels and in the ping-pong kernel
     without a workspace; per KV head from the pre-pass when the ping-pong
-    kernel has one, as prefill_attention gives it) and O is tracked as
-    acc * 2^e.
+    kernel has one, as prefill_attention gives it, and the sequence has the
+    2048 queries that enable it) and O is tracked as acc * 2^e.
     Key 300 (tile 4) holds huge/8 and the last two keys +-huge, so the scale
     grows twice along the sequence; queries before key 300 never see a huge
     row but read rows staged by the same wave (tile 4), which must keep the
     2e-3 absolute bound; the others are checked relative to their magnitude."""
     label = f"prefill {kernel} bf16 |v| up to {huge:g}"
     print(label, flush=True)
-    L = 700
+    L = 2112  # >= 2048 queries: the ping-pong kernel takes the V pre-pass
     q, k, v, cu = make_varlen([L], 8, 2, 128, torch.bfloat16, seed=21)
     g = torch.Generator().manual_seed(22)
     for j, f in ((300, huge / 8), (L - 2, -huge), (L - 1, huge)):
@@ -204,11 +204,12 @@ def test_prefill_bf16_with_and_without_workspace():
     """bf16 on the ping-pong kernel with the workspace (V converted to fp16
     by the pre-pass, one scale per KV head) and without it (V converted tile
     by tile in the kernel): bit-identical while every |v| < 2^15 (both scales
-    are 1), and both within the tolerance when a row reaches 1e6."""
+    are 1), and both within the tolerance when a row reaches 1e6.  The
+    sequence has the 2048 queries from which the library runs the pre-pass."""
     from flashattntile_amd import _hip
 
     print("prefill bf16 workspace / no workspace", flush=True)
-    L = 1500
+    L = 2304
     q, k, v, cu = make_varlen([L], 32, 8, 128, torch.bfloat16, seed=31, device=DEV)
     outs = []
     for big in (False, True):
