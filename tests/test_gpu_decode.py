@@ -304,3 +304,33 @@ def test_auto_partition_skewed_batch():
     out = paged_decode_attention(q, cache)
     torch.cuda.synchronize()
     assert_parity(out, _ref32(q, cache), label="auto partition skewed")
+
+
+@pytest.mark.parametrize("layout", ["transposed", "every_other_column"])
+def test_decode_strided_page_table_and_seq_lens(layout):
+    """A page table whose columns are not unit-strided (a transposed layout,
+    or every second column of a wider table) and a strided seq_lens give the
+    contiguous launch's exact bits: the wrapper makes them dense before the
+    kernel reads them (the reference honours any strides, kernels/decode.py:89).
+    DecodeLaunch, which keeps raw pointers across runs, refuses them."""
+    from flashattntile_amd.kernels.decode import DecodeLaunch
+
+    q, cache = _case([700, 33, 1, 400], 8, 2, 128, 16, torch.float16, seed=41)
+    pt, sl = cache.page_table, cache.seq_lens
+    if layout == "transposed":
+        pt_s = pt.t().contiguous().t()
+    else:
+        wide = torch.full((pt.shape[0], 2 * pt.shape[1]), -7, dtype=torch.int32, device=DEV)
+        wide[:, ::2] = pt
+        pt_s = wide[:, ::2]
+    sl_s = torch.stack([sl, torch.full_like(sl, 99999)], dim=1)[:, 0]
+    assert pt_s.stride(-1) != 1 and not sl_s.is_contiguous() and torch.equal(pt_s, pt) and torch.equal(sl_s, sl)
+    strided = PagedKVCache(cache.k_cache, cache.v_cache, pt_s, sl_s, cache.page_size)
+    for split in (1, 3):
+        want = paged_decode_attention(q, cache, config={"split_k": split})
+        got = paged_decode_attention(q, strided, config={"split_k": split})
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (layout, split)
+    assert_parity(got, _ref32(q, cache), label=f"decode strided table {layout}")
+    with pytest.raises(ValueError, match="contiguous"):
+        DecodeLaunch(q, strided)
