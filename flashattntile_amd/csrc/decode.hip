@@ -135,6 +135,37 @@ __device__ __forceinline__ void k8_exact_f16(const u32x4& raw, u32 (&out)[8]) {
   }
 }
 
+// Page ids of the first unit of keys a wave reads (rows first_row + i * RPL
+// of its partition, i < N), loaded at kernel start together with seq_len when
+// the partition's first page does not depend on seq_len (partition 0, or
+// fixed-size partitions): the first K/V loads then wait one memory latency
+// after the launch instead of two.  The indices are clamped into the table
+// row.  Two empty asm statements order the loads: the sequence index passes
+// through one with the table indices (so the seq_len load issues no earlier
+// than the id loads, not ahead of argument loads they wait for), and seq_len
+// through one with the ids (so the ids are loaded before seq_len's first use
+// instead of where they are used, after the wait for seq_len).  Neither is
+// volatile or touches memory, so the loads, and later table reads, stay
+// scalar loads.
+template <int N, int RPL>
+__device__ __forceinline__ int first_page_ids(int* pid, const int32_t* ptrow, const DecodeParams& p, int split,
+                                              int first_row, int b, bool early) {
+  if (!early) return p.lens[b];
+  const int64_t pg0 = p.pps_fixed > 0 ? (int64_t)split * p.pps_fixed : 0;
+  int64_t idx[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    idx[i] = min(pg0 + ((first_row + i * RPL) >> p.log2P), (int64_t)p.max_pages - 1);
+    asm("" : "+s"(b) : "s"(idx[i]));
+  }
+  int seq_len = p.lens[b];
+#pragma unroll
+  for (int i = 0; i < N; ++i) pid[i] = ptrow[idx[i]];
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm("" : "+s"(pid[i]), "+s"(seq_len));
+  return seq_len;
+}
+
 template <typename QT, int KV, int D, int HG, int NW>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
   using Gm = Geom<KV, D>;
@@ -166,8 +197,15 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   const int r = lane / LPR;
   const int c = lane % LPR;
 
+  // Page ids of this wave's first unit, read together with seq_len when
+  // `early` (first_page_ids); rows of that unit past the sequence's end read
+  // the table again (fetch).
+  constexpr int UL = Gm::kUnitLog2;
+  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
+  const bool early = split == 0 || p.pps_fixed > 0;
+  int first_pid[NI];
   // Partition of this sequence's pages (decode.py:271-276 semantics).
-  int seq_len = p.lens[b];
+  int seq_len = first_page_ids<NI, RPL>(first_pid, ptrow, p, split, w << UL, b, early);
   seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
   const int np = (seq_len + p.P - 1) >> p.log2P;
   const int pps = p.pps_fixed > 0 ? p.pps_fixed : (np + S - 1) / S;
@@ -175,7 +213,6 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
   const int pe = split == S - 1 ? np : min(np, pb + pps);
   const int t_begin = pb << p.log2P;
   const int t_end = min(seq_len, pe << p.log2P);
-  constexpr int UL = Gm::kUnitLog2;
   const int n_units = t_end > t_begin ? (t_end - t_begin + Gm::kUnit - 1) >> UL : 0;
 
   // q for the HG heads, packed pairs of QT (padded heads reuse head0).
@@ -194,18 +231,19 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     }
   }
 
-  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
   const int64_t kv_head_off_k = (int64_t)kvh * p.k_sh + c * EPL;
   const int64_t kv_head_off_v = (int64_t)kvh * p.v_sh + c * EPL;
   constexpr int EB = Gm::kElemBytes;
 
-  auto fetch = [&](UnitRegs<NI>& R, int u) {
+  // first: u is this wave's first unit (first_pid holds its page ids).
+  auto fetch = [&](UnitRegs<NI>& R, int u, bool first) {
     const int base = t_begin + (u << UL);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       int rs = base + i * RPL;
-      if (rs >= t_end) rs = (t_end - 1) & ~(RPL - 1);
-      int phys = ptrow[rs >> p.log2P];
+      const bool past = rs >= t_end;
+      if (past) rs = (t_end - 1) & ~(RPL - 1);
+      int phys = first && early && !past ? first_pid[i] : ptrow[rs >> p.log2P];
       phys = min(max(phys, 0), p.num_pages - 1);
       const int tok = min(rs + r, t_end - 1);
       const int slot = tok & (p.P - 1);
@@ -256,11 +294,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
 
   UnitRegs<NI> nxt;
-  if (w < n_units) fetch(nxt, w);
+  if (w < n_units) fetch(nxt, w, true);
 
   for (int u = w; u < n_units; u += NW) {
     const UnitRegs<NI> cur = nxt;
-    if (u + NW < n_units) fetch(nxt, u + NW);
+    if (u + NW < n_units) fetch(nxt, u + NW, false);
     const int base = t_begin + (u << UL);
 
     // ---- scores: partial q.k over this lane's EPL dims ----
@@ -504,7 +542,12 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
   const int li = lane & 31;  // key row (A operand) / (head, token) column (B, S^T)
   const int g = lane >> 5;   // k-group: head dims 16ks + 8g .. +7 of k-step ks
 
-  int seq_len = p.lens[b];
+  // Page ids of this wave's first 32-key block, read together with seq_len
+  // when `early` (first_page_ids).
+  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
+  const bool early = split == 0 || p.pps_fixed > 0;
+  int first_pid[NLD];
+  int seq_len = first_page_ids<NLD, RPL>(first_pid, ptrow, p, split, w << 5, b, early);
   seq_len = max(0, min(seq_len, p.max_pages << p.log2P));
   const int np = (seq_len + p.P - 1) >> p.log2P;
   const int pps = p.pps_fixed > 0 ? p.pps_fixed : (np + S - 1) / S;
@@ -527,7 +570,6 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
   }
 
-  const int32_t* ptrow = p.pt + (int64_t)b * p.pt_sb;
   const int lrow = lane / CPR;  // this lane's row inside each load
   const int lcol = lane % CPR;  // and its 16-byte chunk
   const int64_t koff = (int64_t)kvh * p.k_sh + lcol * EPC;
@@ -540,13 +582,15 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
     u32x4 k[NLD], v[NLD];
     float ksc[NLD], vsc[NLD];
   };
-  auto fetch = [&](Raw& R, int blk) {
+  // first: blk is this wave's first block (first_pid holds its page ids).
+  auto fetch = [&](Raw& R, int blk, bool first) {
     const int kb = t_begin + (blk << 5);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       int rs = kb + i * RPL;
-      if (rs >= t_end) rs = (t_end - 1) & ~(RPL - 1);
-      int phys = ptrow[rs >> p.log2P];
+      const bool past = rs >= t_end;
+      if (past) rs = (t_end - 1) & ~(RPL - 1);
+      int phys = first && early && !past ? first_pid[i] : ptrow[rs >> p.log2P];
       phys = min(max(phys, 0), p.num_pages - 1);
       const int slot = min(rs + lrow, t_end - 1) & (p.P - 1);
       R.k[i] = *reinterpret_cast<const u32x4*>(p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + koff));
@@ -649,7 +693,7 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
         put(&Vt[row * V_RS + lcol * EPC], R.v[i], R.vsc[i]);
       }
     }
-    if (nxt < n_blocks) fetch(R, nxt);
+    if (nxt < n_blocks) fetch(R, nxt, false);
     wave_lds_fence();
     // S^T = K Q^T for the 32 keys of this block: A = K rows li, dims 16ks + 8g.
     f32x16 s;
@@ -717,7 +761,7 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
     wave_lds_fence();
   };
   Raw R;
-  if (w < n_blocks) fetch(R, w);
+  if (w < n_blocks) fetch(R, w, true);
   for (int blk = w; blk < n_blocks; blk += NW) compute(R, blk, blk + NW);
 
   // ---- merge the waves: O = sum_w acc_w 2^(m_w - M) / sum_w l_w 2^(m_w - M) ----

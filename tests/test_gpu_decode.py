@@ -276,16 +276,20 @@ def test_native_library_is_the_path():
         assert "libfat_hip.so" in fh.read()
 
 
+@pytest.mark.parametrize("kern", ["valu", "mfma"])
 @pytest.mark.parametrize("split_k,pps", [(4, 16), (2, 8), (8, 3), (1, 5), (3, 200)])
-def test_fixed_pages_per_split(split_k, pps):
+def test_fixed_pages_per_split(split_k, pps, kern):
     """Fixed-size partitions (pages_per_split > 0): equal to the oracle whether
     split_k * pages_per_split covers the longest sequence or falls short (then
-    the last partition takes the remaining pages)."""
-    label = f"decode fixed partitions sk{split_k} pps{pps}"
+    the last partition takes the remaining pages).  Every partition of a fixed
+    size reads its first page ids before seq_len is known; sequences of 5, 16
+    and 37 tokens end inside a wave's first unit, and partitions past a
+    sequence's end read nothing."""
+    label = f"decode fixed partitions {kern} sk{split_k} pps{pps}"
     print(label, flush=True)
     lens = [5, 1000, 37, 4096, 16, 2500]
     q, cache = _case(lens, 32, 8, 128, 16, torch.float16, seed=50 + pps)
-    out = paged_decode_attention(q, cache, config={"split_k": split_k, "pages_per_split": pps})
+    out = paged_decode_attention(q, cache, config={"split_k": split_k, "pages_per_split": pps, "kernel": kern})
     torch.cuda.synchronize()
     assert_parity(out, _ref32(q, cache), label=label)
 
