@@ -143,6 +143,39 @@ def test_prefill_long_sequence_head_subsets(seqlen, dtype, kernel):
         assert_parity(out[:, hs], ref, label=f"{label} kv{kvh}")
 
 
+def _first_and_last_rows_ref(q, k, v, L, n, kvh):
+    """fp32 oracle for query rows [0, n) and [L - n, L) of one causal
+    L-token sequence (the query heads of KV head kvh): the first n rows see
+    only the first n tokens, and under bottom-right alignment the last n rows
+    are exactly an n-query prefill over all L keys."""
+    hs = slice(4 * kvh, 4 * kvh + 4)
+    kk, vv = k[:, kvh:kvh + 1].cpu().contiguous(), v[:, kvh:kvh + 1].cpu().contiguous()
+    cu_n = torch.tensor([0, n], dtype=torch.int32)
+    cu_l = torch.tensor([0, L], dtype=torch.int32)
+    first = ref_attention_varlen(q[:n, hs].cpu().contiguous(), kk[:n].contiguous(), vv[:n].contiguous(), cu_n, cu_n,
+                                 causal=True, return_fp32=True)
+    last = ref_attention_varlen(q[L - n:, hs].cpu().contiguous(), kk, vv, cu_n, cu_l, causal=True, return_fp32=True)
+    return hs, first, last
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_32k_sequence_first_and_last_rows(dtype):
+    """One causal sequence of 32768 tokens (32/8 heads, D128), four times
+    BASELINE's longest prefill: the kernels address K/V with 32-bit offsets
+    per sequence and run 128 query blocks per head.  The first and last 256
+    rows of KV heads 0 and 7 against the fp32 oracle."""
+    L, n = 32768, 256
+    label = f"prefill 32k {dtype}"
+    print(label, flush=True)
+    q, k, v, cu = make_varlen([L], 32, 8, 128, dtype, seed=32, device=DEV)
+    out = prefill_attention(q, k, v, cu, cu, L, L, causal=True)
+    torch.cuda.synchronize()
+    for kvh in (0, 7):
+        hs, first, last = _first_and_last_rows_ref(q, k, v, L, n, kvh)
+        assert_parity(out[:n, hs], first, label=f"{label} kv{kvh} first rows")
+        assert_parity(out[L - n:, hs], last, label=f"{label} kv{kvh} last rows")
+
+
 def test_prefill_launch_into_strided_output():
     """prefill_launch writes into a caller-provided (head-strided) buffer."""
     print("prefill strided out", flush=True)

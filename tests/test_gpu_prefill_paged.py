@@ -18,7 +18,7 @@ from _parity import assert_parity, force_prefill_knobs, make_paged
 from flashattntile_amd import PagedKVCache
 from flashattntile_amd.kernels.prefill import paged_prefill_attention, prefill_attention
 from flashattntile_amd.paging import gather_contiguous
-from oracle.reference import ref_attention_paged_prefill
+from oracle.reference import ref_attention_paged_prefill, ref_attention_varlen
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -108,6 +108,31 @@ def test_paged_prefill_equals_packed_prefill(dtype, kernel):
     out_packed = prefill_attention(q, pk, pv, cu, cu, max(lens), max(lens), causal=True)
     torch.cuda.synchronize()
     assert torch.equal(out_paged, out_packed)
+
+
+def test_paged_prefill_32k_sequence_first_and_last_rows():
+    """One causal fp16 sequence of 32768 tokens (2048 pages of 16, permuted)
+    read through the page table: the first and last 256 rows of KV heads 0
+    and 7 against the fp32 oracle on the gathered keys (the first rows see
+    the first 256 tokens only; the last rows, bottom-right aligned, all)."""
+    L, n = 32768, 256
+    print("paged prefill 32k", flush=True)
+    q, cache, cu = _case([L], [L], 32, 8, 128, 16, torch.float16, seed=32)
+    out = paged_prefill_attention(q, cache, cu, L, causal=True)
+    torch.cuda.synchronize()
+    k, v = gather_contiguous(cache)
+    k, v = k[0, :L], v[0, :L]
+    cu_n = torch.tensor([0, n], dtype=torch.int32)
+    cu_l = torch.tensor([0, L], dtype=torch.int32)
+    for kvh in (0, 7):
+        hs = slice(4 * kvh, 4 * kvh + 4)
+        kk, vv = k[:, kvh:kvh + 1].cpu().contiguous(), v[:, kvh:kvh + 1].cpu().contiguous()
+        first = ref_attention_varlen(q[:n, hs].cpu().contiguous(), kk[:n].contiguous(), vv[:n].contiguous(), cu_n,
+                                     cu_n, causal=True, return_fp32=True)
+        last = ref_attention_varlen(q[L - n:, hs].cpu().contiguous(), kk, vv, cu_n, cu_l, causal=True,
+                                    return_fp32=True)
+        assert_parity(out[:n, hs], first, label=f"paged prefill 32k kv{kvh} first rows")
+        assert_parity(out[L - n:, hs], last, label=f"paged prefill 32k kv{kvh} last rows")
 
 
 def test_paged_prefill_chunked_equals_one_shot(kernel):
