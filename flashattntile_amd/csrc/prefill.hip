@@ -281,6 +281,53 @@ constexpr float kLazy = 8.0f;
 #define FAT_PF_SPLIT_LONG 32
 #endif
 
+// Epilogue of a wave that owns 32 query rows (row0 ..): O = acc / l (times
+// 2^e_acc for bf16) to the output, through `lds` (this wave's 32 rows of
+// D + 8 elements at lds + w * 32 * (D + 8), not read by any other wave):
+// the wave writes its O^T fragments there as T, then each lane stores 16
+// contiguous bytes of a row (8-byte pieces when the output rows are not
+// 16-byte aligned).
+template <typename T, int D, int DB>
+__device__ __forceinline__ void write_rows_via_lds(uint16_t* lds, int w, int li, int g, int lane, const f32x16 (&acc)[DB],
+                                                   float l_run, int e_acc, bool vh, const PrefillParams& p,
+                                                   int q_start, int q_len, int h, int row0) {
+  constexpr int OS = D + 8;  // row stride (elements)
+  const float l_tot = xor32<OpAdd>(l_run);
+  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (vh) inv *= as_f32((u32)(127 + e_acc) << 23);
+  uint16_t* ob = lds + w * 32 * OS;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int d0 = 32 * db + 4 * g + 8 * rr;
+      u32x2 pk;
+      pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
+      pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
+      *reinterpret_cast<u32x2*>(&ob[li * OS + d0]) = pk;
+    }
+  wave_lds_fence();
+  constexpr int CPR_O = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR_O;  // rows per store instruction
+  const int oc = lane % CPR_O;
+  const int orow = lane / CPR_O;
+  const bool o16 = ((reinterpret_cast<uintptr_t>(p.out) | (uintptr_t)(2 * p.o_st) | (uintptr_t)(2 * p.o_sh)) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = i * RPI + orow;
+    const u32x4 val = *reinterpret_cast<const u32x4*>(&ob[r * OS + 8 * oc]);
+    if (row0 + r < q_len) {
+      uint8_t* dst = p.out + 2 * ((int64_t)(q_start + row0 + r) * p.o_st + (int64_t)h * p.o_sh + 8 * oc);
+      if (o16) {
+        *reinterpret_cast<u32x4*>(dst) = val;
+      } else {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{val[0], val[1]};
+        *reinterpret_cast<u32x2*>(dst + 8) = u32x2{val[2], val[3]};
+      }
+    }
+  }
+}
+
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
 // NG = 2: two groups of 4 waves take alternate K/V tiles for the same query
@@ -684,23 +731,12 @@ void prefill_kernel(const PrefillParams p) {
       for (int r = 0; r < 16; ++r) acc[db][r] = acc[db][r] * o0 + xch[64 * (16 * db + r)] * o1;
   }
 
-  // ---- epilogue: O = O^T / l, lane writes 4 consecutive dims per store ----
-  const float l_tot = xor32<OpAdd>(l_run);
-  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if constexpr (VH) inv *= as_f32((u32)(127 + e_acc) << 23);
-  if (my_row < q_len) {
-    uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int d0 = 32 * db + 4 * g + 8 * rr;
-        u32x2 pk;
-        pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
-        pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + 2 * d0) = pk;
-      }
-  }
+  // ---- epilogue: O = O^T / l.  Each wave stages its 32 rows (as T,
+  // row-major) in a wave-private LDS area and stores them row by row, 16
+  // contiguous bytes per lane, so an output row leaves in whole cache lines
+  // (writing O^T directly puts 8-byte pieces of 32 rows in every store).
+  if constexpr (NG == 1) __syncthreads();  // every wave is done with the V tiles
+  write_rows_via_lds<T, D, DB>(&Vs[0][0][0], w, li, g, lane, acc, l_run, e_acc, VH, p, q_start, q_len, h, row0);
 }
 
 
