@@ -282,20 +282,20 @@ constexpr float kLazy = 8.0f;
 #endif
 
 // Epilogue of a wave that owns 32 query rows (row0 ..): O = acc / l (times
-// 2^e_acc for bf16) to the output, through `lds` (this wave's 32 rows of
-// D + 8 elements at lds + w * 32 * (D + 8), not read by any other wave):
-// the wave writes its O^T fragments there as T, then each lane stores 16
-// contiguous bytes of a row (8-byte pieces when the output rows are not
-// 16-byte aligned).
+// 2^e_acc for bf16) to the output, through `ob`, an LDS area of
+// kOutStage<D> elements (32 rows of D + 8) that no other wave touches
+// meanwhile: the wave writes its O^T fragments there as T, then each lane
+// stores 16 contiguous bytes of a row (8-byte pieces when the output rows
+// are not 16-byte aligned).
+template <int D> constexpr int kOutStage = 32 * (D + 8);
 template <typename T, int D, int DB>
-__device__ __forceinline__ void write_rows_via_lds(uint16_t* lds, int w, int li, int g, int lane, const f32x16 (&acc)[DB],
+__device__ __forceinline__ void write_rows_via_lds(uint16_t* ob, int li, int g, int lane, const f32x16 (&acc)[DB],
                                                    float l_run, int e_acc, bool vh, const PrefillParams& p,
                                                    int q_start, int q_len, int h, int row0) {
   constexpr int OS = D + 8;  // row stride (elements)
   const float l_tot = xor32<OpAdd>(l_run);
   float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (vh) inv *= as_f32((u32)(127 + e_acc) << 23);
-  uint16_t* ob = lds + w * 32 * OS;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -735,8 +735,10 @@ void prefill_kernel(const PrefillParams p) {
   // row-major) in a wave-private LDS area and stores them row by row, 16
   // contiguous bytes per lane, so an output row leaves in whole cache lines
   // (writing O^T directly puts 8-byte pieces of 32 rows in every store).
+  static_assert(sizeof(Vs[0]) >= 4 * kOutStage<D> * sizeof(uint16_t), "output staging");
   if constexpr (NG == 1) __syncthreads();  // every wave is done with the V tiles
-  write_rows_via_lds<T, D, DB>(&Vs[0][0][0], w, li, g, lane, acc, l_run, e_acc, VH, p, q_start, q_len, h, row0);
+  write_rows_via_lds<T, D, DB>(&Vs[0][0][0] + w * kOutStage<D>, li, g, lane, acc, l_run, e_acc, VH, p, q_start,
+                               q_len, h, row0);
 }
 
 
@@ -1123,22 +1125,13 @@ void prefill_pp_kernel(const PrefillParams p) {
     if (grp == 0) __syncthreads();
   }
 
-  const float l_tot = xor32<OpAdd>(l_run);
-  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if constexpr (VH) inv *= as_f32((u32)(127 + e_acc) << 23);
-  if (my_row < q_len) {
-    uint8_t* op = p.out + 2 * ((int64_t)(q_start + my_row) * p.o_st + (int64_t)h * p.o_sh);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int d0 = 32 * db + 4 * g + 8 * rr;
-        u32x2 pk;
-        pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
-        pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + 2 * d0) = pk;
-      }
-  }
+  // Epilogue: waves 0-3 stage their output rows in the K buffers, waves 4-7
+  // in the V buffers, once every wave is done with the tiles.
+  static_assert(sizeof(Ks) >= 4 * kOutStage<D> * sizeof(uint16_t), "output staging");
+  static_assert(sizeof(Vs) >= 4 * kOutStage<D> * sizeof(uint16_t), "output staging");
+  __syncthreads();
+  write_rows_via_lds<T, D, DB>((w < 4 ? &Ks[0][0] : &Vs[0][0]) + (w & 3) * kOutStage<D>, li, g, lane, acc, l_run,
+                               e_acc, VH, p, q_start, q_len, h, row0);
 }
 
 // ---------------------------------------------------------------------------
