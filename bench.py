@@ -27,6 +27,7 @@ the table to ``--report`` (JSON) as well as stderr.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -345,8 +346,14 @@ def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7,
     need = _hip.prefill_workspace_bytes(k.shape[0], hkv, d) if dtype == torch.bfloat16 else 0
     ws = torch.empty(need, dtype=torch.uint8, device=device) if need else None
 
+    # The argument block is built once: a step is one ctypes call, so rows
+    # whose kernel takes ~15 us are not bound by Python building it.
+    args = _hip.prefill_args(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, workspace=ws)
+    launch, ref, hs = _hip.lib().fat_prefill_varlen, ctypes.byref(args), ctypes.c_void_p(handle)
+
     def step(i):
-        _hip.prefill_varlen(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, workspace=ws, stream=handle)
+        if launch(ref, hs) != 0:
+            raise RuntimeError(_hip.lib().fat_last_error().decode(errors="replace"))
 
     flops = flops_attention_varlen(hq, d, lens, lens, causal=True)
     extra = {}

@@ -471,6 +471,29 @@ def prefill_varlen(
     kernel: int = KERNEL_AUTO,
 ) -> None:
     """Enqueue ``fat_prefill_varlen`` for already-validated device tensors."""
+    a = prefill_args(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k, causal,
+                     softmax_scale, workspace=workspace, kernel=kernel)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
+
+
+def prefill_args(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    out: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    causal: bool,
+    softmax_scale: float,
+    workspace: torch.Tensor | None = None,
+    kernel: int = KERNEL_AUTO,
+) -> PrefillArgs:
+    """The ``fat_prefill_args`` block of a packed prefill launch (see
+    prefill_varlen).  It holds the tensors' addresses: they must stay alive
+    and in place while the block is used."""
     a = PrefillArgs()
     a.q = _ptr(q)
     a.k = _ptr(k)
@@ -495,8 +518,7 @@ def prefill_varlen(
     a.dtype = dtype_code(q.dtype)
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
-    handle = current_stream_handle(q.device) if stream is None else stream
-    _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
+    return a
 
 
 def prefill_paged(
