@@ -188,6 +188,23 @@ def test_prefill_launch_into_strided_output():
     assert_parity(out, _ref32(q, k, v, cu, cu, True), label="strided out")
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_output_rows_only_8_byte_aligned(dtype, d, kernel):
+    """Output rows that start 8 bytes past a 16-byte boundary (base offset 4
+    elements, head stride d + 4): the kernels store each row in 8-byte pieces
+    there, and the 4-element gaps between heads stay untouched."""
+    print(f"prefill 8-byte-aligned out {dtype} D{d} {kernel}", flush=True)
+    q, k, v, cu = make_varlen([300, 77, 129], 8, 2, d, dtype, seed=5, device=DEV)
+    big = torch.zeros(q.shape[0], 8, d + 4, dtype=dtype, device=DEV)
+    out = big[:, :, 4:]
+    assert out.data_ptr() % 16 == 8 and (out.stride(1) * out.element_size()) % 16 == 8
+    prefill_launch(q, k, v, cu, cu, 300, 300, True, d ** -0.5, out=out, kernel=None if kernel == "auto" else kernel)
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :, :4] == 0)
+    assert_parity(out, _ref32(q, k, v, cu, cu, True), label=f"8-byte-aligned out D{d} {kernel}")
+
+
 def test_ops_compile_on_device():
     """The custom ops inside a torch.compile(fullgraph=True) graph on the GPU."""
     print("prefill compile", flush=True)
