@@ -11,6 +11,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 from flashattntile_amd import _hip
 
@@ -153,6 +154,30 @@ def test_prefill_argument_errors_are_reported():
     assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "kernel" in _err()
     p.kernel, p.rows = _hip.KERNEL_AUTO, 3
     assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "rows" in _err()
+
+
+def test_prefill_args_block_fields():
+    """prefill_args fills the fat_prefill_args block from the tensors
+    (addresses, element strides, shape, dtype code, scale, kernel) without a
+    launch; a head-strided output keeps its own strides."""
+    q = torch.zeros(30, 8, 64, dtype=torch.bfloat16)
+    k = torch.zeros(50, 2, 64, dtype=torch.bfloat16)
+    v = torch.zeros(50, 2, 64, dtype=torch.bfloat16)
+    cq = torch.tensor([0, 10, 30], dtype=torch.int32)
+    ck = torch.tensor([0, 20, 50], dtype=torch.int32)
+    out = torch.zeros(30, 8, 72, dtype=torch.bfloat16)[:, :, 4:68]
+    ws = torch.zeros(512, dtype=torch.uint8)
+    a = _hip.prefill_args(q, k, v, cq, ck, out, 20, 30, True, 0.125, workspace=ws,
+                          kernel=_hip.KERNEL_PREFILL_PINGPONG)
+    assert (a.q, a.k, a.v, a.out, a.workspace) == (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                                   ws.data_ptr())
+    assert (a.cu_seqlens_q, a.cu_seqlens_k) == (cq.data_ptr(), ck.data_ptr())
+    assert (a.q_stride_t, a.q_stride_h, a.k_stride_t, a.k_stride_h) == (512, 64, 128, 64)
+    assert (a.out_stride_t, a.out_stride_h) == (8 * 72, 72)
+    assert (a.batch, a.total_q, a.total_k, a.num_heads, a.num_kv_heads, a.head_dim) == (2, 30, 50, 8, 2, 64)
+    assert (a.max_seqlen_q, a.max_seqlen_k, a.causal, a.dtype) == (20, 30, 1, _hip.DT_BF16)
+    assert a.softmax_scale == 0.125 and a.kernel == _hip.KERNEL_PREFILL_PINGPONG
+    assert _hip.prefill_args(q, k, v, cq, ck, q, 20, 30, False, 0.5).workspace is None
 
 
 def test_quantize_argument_errors_are_reported():
