@@ -226,3 +226,22 @@ def test_prefill_paged_op_and_backend_route():
                                                          max_seqlen_q=max(lens_q), softmax_scale=0.09))
     torch.cuda.synchronize()
     assert torch.equal(got, want) and torch.equal(compiled, want) and torch.equal(routed, want)
+
+
+@pytest.mark.parametrize("P", [4, 16])
+@pytest.mark.parametrize("kern", [None, "pingpong", "4wave", "4wave_split"])
+def test_paged_prefill_output_rows_only_8_byte_aligned(kern, P):
+    """Paged prefill into output rows that start 8 bytes past a 16-byte
+    boundary (base offset 4 elements, head stride 68): each row leaves in
+    8-byte pieces and the gaps between heads stay untouched."""
+    from flashattntile_amd.kernels.prefill import paged_prefill_launch
+
+    print(f"paged prefill 8-byte-aligned out {kern or 'auto'} P{P}", flush=True)
+    q, cache, cu = _case([300, 517, 64], [300, 200, 64], 8, 2, 64, P, torch.float16, seed=9)
+    big = torch.zeros(q.shape[0], 8, 68, dtype=q.dtype, device=DEV)
+    out = big[:, :, 4:]
+    assert out.data_ptr() % 16 == 8
+    paged_prefill_launch(q, cache, cu, 300, True, 64 ** -0.5, out=out, kernel=kern)
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :, :4] == 0)
+    assert_parity(out, _ref32(q, cache, cu, True, scale=64 ** -0.5), label=f"paged 8-byte-aligned out {kern} P{P}")
