@@ -156,6 +156,9 @@ ROW_WARM_MS = 0.0
 # many ms of the same launches.
 SUSTAIN_MS = 200.0
 
+# Seconds of GPU idle before a timed leg when no CPU baseline runs there.
+IDLE_GAP_S = 10.0
+
 
 def _prewarm(fn, stream, warm_ms=None):
     """Run ``fn`` back to back until ``warm_ms`` (default ROW_WARM_MS) of GPU
@@ -331,9 +334,10 @@ def _prefill_case(lens, hq, hkv, d, dtype, seed, device):
 
 
 def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7, sustain_ms=None):
-    """Prefill TFLOP/s over `steps` back-to-back launches.  With `sustain_ms`
-    the launches are timed twice: right after `warmup` (from an idle GPU,
-    `cold_*`) and again after `sustain_ms` of load (the main figures)."""
+    """Prefill TFLOP/s over `steps` back-to-back launches after `warmup`
+    untimed ones (the contract's timing; without `sustain_ms` the row's own
+    ROW_WARM_MS of launches come first).  With `sustain_ms` the same steps are
+    timed again after that many ms of load (`sustained_*`)."""
     from flashattntile_amd import _hip
     from flashattntile_amd.autotune import flops_attention_varlen
 
@@ -342,13 +346,15 @@ def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7,
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
     mx = max(lens)
-    # the workspace the product path (kernels/prefill.py:prefill_launch) passes
-    need = _hip.prefill_workspace_bytes(k.shape[0], hkv, d) if dtype == torch.bfloat16 else 0
-    ws = torch.empty(need, dtype=torch.uint8, device=device) if need else None
-
     # The argument block is built once: a step is one ctypes call, so rows
-    # whose kernel takes ~15 us are not bound by Python building it.
-    args = _hip.prefill_args(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5, workspace=ws)
+    # whose kernel takes ~15 us are not bound by Python building it.  The
+    # workspace is the one the product path (kernels/prefill.py:
+    # prefill_launch) passes: what the library says this launch uses.
+    args = _hip.prefill_args(q, k, v, cu, cu, out, mx, mx, True, d ** -0.5)
+    need = _hip.prefill_varlen_workspace_bytes(args)
+    ws = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+    if ws is not None:
+        args.workspace = ws.data_ptr()
     launch, ref, hs = _hip.lib().fat_prefill_varlen, ctypes.byref(args), ctypes.c_void_p(handle)
 
     def step(i):
@@ -356,39 +362,44 @@ def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7,
             raise RuntimeError(_hip.lib().fat_last_error().decode(errors="replace"))
 
     flops = flops_attention_varlen(hq, d, lens, lens, causal=True)
-    extra = {}
+    extra = {"workspace_bytes": need}
     if sustain_ms is not None:
-        ms_cold = _time_steps(step, steps, warmup, stream, warm_ms=0.0)
-        extra = {"cold_ms": ms_cold, "cold_tflops": flops / (ms_cold * 1e-3) / 1e12}
-        ms = _time_steps(step, steps, 0, stream, warm_ms=sustain_ms)
+        ms = _time_steps(step, steps, warmup, stream, warm_ms=0.0)
+        ms_sus = _time_steps(step, steps, 0, stream, warm_ms=sustain_ms)
+        extra.update(sustained_ms=ms_sus, sustained_tflops=flops / (ms_sus * 1e-3) / 1e12)
     else:
         ms = _time_steps(step, steps, warmup, stream)
     tflops = flops / (ms * 1e-3) / 1e12
     return {"ms": ms, "tflops": tflops, "flops": flops, "frac": tflops / MFMA_PEAK_TFLOPS, **extra}
 
 
-def bench_prefill(args, device, seq=8192):
-    res = {}
+PREFILL_SEQ = 8192
+
+
+def bench_prefill_leg(args, device, name, dtype, seq=PREFILL_SEQ):
+    """One dtype of the prefill leg, timed as the decode headline is: the
+    contract's steps right after the warm-up steps (the main figures and the
+    roofline), then the same steps after SUSTAIN_MS of load (`sustained`)."""
     steps = max(10, args.steps // 10)
-    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
-        r = run_prefill([seq], dt, device, steps, max(3, args.warmup // 4), sustain_ms=SUSTAIN_MS)
-        res[name] = {
-            "ms": round(r["ms"], 4),
-            "tflops": round(r["tflops"], 1),
-            "first_after_idle": {"ms": round(r["cold_ms"], 4), "tflops": round(r["cold_tflops"], 1),
-                                 "frac": round(r["cold_tflops"] / MFMA_PEAK_TFLOPS, 4)},
-            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"],
-                         "traffic": (_traffic_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128")
-                                     if name == "f16" else None),
-                         "mfma_busy": _mfma_busy_from_profiles(f"prefill_causal_seq{seq}_h32_kv8_d128", name),
-                         "counters_source": _profile_entry(f"prefill_causal_seq{seq}_h32_kv8_d128")[1]},
-        }
-    res["workload"] = f"prefill_causal_seq{seq}_h32_kv8_d128"
-    res["steps"] = steps
-    res["timing"] = (f"main figures after {SUSTAIN_MS:.0f} ms of the same launches (sustained load); "
-                     "first_after_idle: the same steps right after the warm-up steps")
-    return res
+    warmup = max(3, args.warmup // 4)
+    r = run_prefill([seq], dtype, device, steps, warmup, sustain_ms=SUSTAIN_MS)
+    workload = f"prefill_causal_seq{seq}_h32_kv8_d128"
+    entry_wl = workload if name == "f16" else f"{workload}_bf16"
+    return {
+        "workload": entry_wl,
+        "steps": steps,
+        "warmup": warmup,
+        "ms": round(r["ms"], 4),
+        "tflops": round(r["tflops"], 1),
+        "workspace_bytes": r["workspace_bytes"],
+        "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(r["frac"], 4), "flops_per_launch": r["flops"],
+                     "traffic": _traffic_from_profiles(entry_wl),
+                     "mfma_busy": _profile_entry(entry_wl)[0].get("mfma_busy"),
+                     "counters_source": _profile_entry(entry_wl)[1]},
+        "sustained": {"ms": round(r["sustained_ms"], 4), "tflops": round(r["sustained_tflops"], 1),
+                      "frac": round(r["sustained_tflops"] / MFMA_PEAK_TFLOPS, 4), "after_ms_of_load": SUSTAIN_MS},
+    }
 
 
 def cpu_baseline_decode(budget_s=12.0):
@@ -418,6 +429,85 @@ def cpu_baseline_decode(budget_s=12.0):
         "host": host,
         "ms": best * 1e3,
     }
+
+
+def cpu_baseline_prefill(budget_s=8.0, seq=PREFILL_SEQ):
+    """fp32 oracle (oracle/reference.py ref_attention_varlen) on a bounded
+    sample of the prefill workload: one KV head and its 4 query heads of the
+    causal seq-8192 sequence (fp16 inputs upcast), min over repetitions
+    within ~budget_s.  TFLOP/s counts the same algorithmic causal FLOPs as
+    the GPU figure (flashattn_tile/autotune.py:31-73) for that sample."""
+    from flashattntile_amd.autotune import flops_attention_varlen
+    from oracle.reference import ref_attention_varlen
+
+    host = _host()
+    cores = _cores(host)
+    torch.set_num_threads(cores)
+    q, k, v, cu = _prefill_case([seq], 4, 1, 128, torch.float16, 7, "cpu")
+    best, reps = _time_cpu(lambda: ref_attention_varlen(q, k, v, cu, cu, causal=True), budget_s, max_reps=9)
+    flops = flops_attention_varlen(4, 128, [seq], [seq], causal=True)
+    return {
+        "value": flops / best / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"fp32 oracle ref_attention_varlen on one KV head and its 4 query heads of the causal seq-{seq} "
+                  f"sequence (D128, fp16 inputs upcast): 1/8 of the GPU leg's work; min of {reps} runs after 1 "
+                  f"warm-up; {cores} torch threads",
+        "cpu_model": host.get("cpu_model"),
+        "ms": best * 1e3,
+    }
+
+
+def op_latency_decode(device, reps=100, warmup=25):
+    """Latency of the op-level decode calls at the headline shape, as the
+    reference's benchmark times its wrapper (scripts/benchmark_gpu.py:57-59,
+    178: triton's do_bench, median of 100 calls after 25 warm-ups, cache
+    flushed before each): HIP events around each call, after a 512 MB read
+    that evicts L2 and the Infinity Cache.  Each call includes the wrapper's
+    validation (one device->host sync), the tuned-store lookup and the
+    launch, so this is what a caller of the op waits for per call."""
+    from flashattntile_amd import PagedKVCache
+    from flashattntile_amd.autotune import bytes_decode_paged
+    from flashattntile_amd.kernels.decode import paged_decode_attention, resolve_decode_config
+
+    B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
+    q, pools, table, lens, _, _ = _paged_inputs([CTX] * B, HQ, HKV, D, P, torch.float16, seed=1, device=device)
+    k, v = pools[0][0], pools[0][1]
+    cache = PagedKVCache(k, v, table, lens, P)
+    split = resolve_decode_config(q, cache, CTX, B * (CTX // P))["split_k"]
+    flush = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=device)
+    sink = torch.empty((), dtype=flush.dtype, device=device)
+    stream = torch.cuda.current_stream(device)
+    scale = D ** -0.5
+    calls = {
+        "paged_decode_attention": lambda: paged_decode_attention(q, cache),
+        "torch.ops.flashattn_tile.paged_decode": lambda: torch.ops.flashattn_tile.paged_decode(
+            q, k, v, table, lens, P, scale, split),
+    }
+    res = {}
+    for name, fn in calls.items():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(reps):
+            torch.amax(flush, dim=0, out=sink)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = statistics.median(a.elapsed_time(b) for a, b in evs)
+        res[name] = {"ms": round(ms, 5), "gbs": round(bytes_decode_paged([CTX] * B, HQ, HKV, D) / (ms * 1e-3) / 1e9,
+                                                        1)}
+    res["method"] = (f"HIP events around each call, median of {reps} after {warmup} warm-ups, each after a "
+                     f"{FLUSH_BYTES >> 20} MB read; split_k {split} (the launch the wrapper resolves); validation "
+                     "sync included")
+    del pools, flush
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -985,23 +1075,41 @@ def main():
         legs.discard("prefill")
     if args.no_cpu_baseline:
         legs.discard("cpu")
+
+    def idle_gap(cpu_leg):
+        """Leave the GPU idle before the next timed leg, so that every leg's
+        contract timing starts from an idle GPU as the decode leg's does: the
+        CPU baseline when it runs, else IDLE_GAP_S of sleep."""
+        if cpu_leg is not None and "cpu" in legs:
+            return cpu_leg()
+        time.sleep(IDLE_GAP_S)
+        return None
+
     dec = None
     if "decode" in legs:
         dec = bench_decode(args, device)
         print(f"# decode: {dec['gbs']:.1f} GB/s ({dec['ms'] * 1e3:.1f} us/step, split_k={dec['split_k']}, "
               f"waves={dec['waves_per_group']}); after {SUSTAIN_MS:.0f} ms of load {dec['sustained_gbs']:.1f} GB/s "
               f"({dec['sustained_ms'] * 1e3:.1f} us/step)", file=sys.stderr, flush=True)
+        dec["op_latency"] = op_latency_decode(device)
+        print(f"# decode op latency: {json.dumps(dec['op_latency'])}", file=sys.stderr, flush=True)
+    cpu = idle_gap(lambda: cpu_baseline_decode(args.cpu_budget)) if ("prefill" in legs or "cpu" in legs) else None
+    if cpu is not None:
+        print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} cores", file=sys.stderr, flush=True)
     pre = None
     if "prefill" in legs:
-        pre = bench_prefill(args, device)
-        print(f"# prefill seq8192: fp16 {pre['f16']['tflops']:.1f} TFLOP/s ({pre['f16']['ms']:.3f} ms), "
-              f"bf16 {pre['bf16']['tflops']:.1f} TFLOP/s; first after idle fp16 "
-              f"{pre['f16']['first_after_idle']['tflops']:.1f}, bf16 {pre['bf16']['first_after_idle']['tflops']:.1f}",
-              file=sys.stderr, flush=True)
-    cpu = None
-    if "cpu" in legs:
-        cpu = cpu_baseline_decode(args.cpu_budget)
-        print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} cores", file=sys.stderr, flush=True)
+        pre = {"f16": bench_prefill_leg(args, device, "f16", torch.float16)}
+        cpu_pre = idle_gap(lambda: cpu_baseline_prefill(min(args.cpu_budget, 8.0)))
+        pre["bf16"] = bench_prefill_leg(args, device, "bf16", torch.bfloat16)
+        if cpu_pre is not None:
+            pre["cpu_baseline"] = {k: v for k, v in cpu_pre.items() if k != "ms"}
+        pre["timing"] = (f"each dtype from an idle GPU (after seconds of CPU baseline or {IDLE_GAP_S:.0f} s of "
+                         f"sleep): ms / tflops / roofline over the contract's steps right after the warm-up steps; "
+                         f"`sustained` the same steps after {SUSTAIN_MS:.0f} ms of load")
+        print(f"# prefill seq{PREFILL_SEQ}: fp16 {pre['f16']['tflops']:.1f} TFLOP/s ({pre['f16']['ms']:.3f} ms), "
+              f"bf16 {pre['bf16']['tflops']:.1f}; sustained fp16 {pre['f16']['sustained']['tflops']:.1f}, "
+              f"bf16 {pre['bf16']['sustained']['tflops']:.1f}"
+              + (f"; cpu {cpu_pre['value']:.3f} TFLOP/s" if cpu_pre else ""), file=sys.stderr, flush=True)
     if dec is None:
         return
 
@@ -1042,6 +1150,7 @@ def main():
                       "frac": round(dec["sustained_gbs"] / HBM_PEAK_GBS, 4), "after_ms_of_load": SUSTAIN_MS,
                       "note": "the same steps timed again after sustained load; `value` is the contract's timing"},
         "cpu_baseline": None if cpu is None else {k: v for k, v in cpu.items() if k != "ms"},
+        "op_latency": dec["op_latency"],
         "prefill": pre,
     }
     if dec["tuning_ms"]:

@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # enum fat_dtype
 DT_F16 = 0
@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "fat_paged_decode",
     "fat_paged_decode_noalloc",
     "fat_prefill_workspace_bytes",
+    "fat_prefill_varlen_workspace_bytes",
     "fat_prefill_varlen",
     "fat_prefill_paged",
     "fat_quantize_pages",
@@ -273,6 +274,10 @@ def _load() -> None:
             _ERROR = f"cannot load {path}: {exc}"
             return
         lib.fat_abi_version.restype = ctypes.c_int
+        version = lib.fat_abi_version()
+        if version != ABI_VERSION:  # before binding: an old build lacks newer symbols
+            _ERROR = f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it"
+            return
         lib.fat_last_error.restype = ctypes.c_char_p
         lib.fat_paged_decode_workspace_bytes.restype = ctypes.c_size_t
         lib.fat_paged_decode_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32, _c_i32]
@@ -282,6 +287,8 @@ def _load() -> None:
         lib.fat_paged_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _c_vp]
         lib.fat_prefill_workspace_bytes.restype = ctypes.c_size_t
         lib.fat_prefill_workspace_bytes.argtypes = [_c_i32, _c_i32, _c_i32]
+        lib.fat_prefill_varlen_workspace_bytes.restype = ctypes.c_size_t
+        lib.fat_prefill_varlen_workspace_bytes.argtypes = [ctypes.POINTER(PrefillArgs)]
         lib.fat_prefill_varlen.restype = ctypes.c_int
         lib.fat_prefill_varlen.argtypes = [ctypes.POINTER(PrefillArgs), _c_vp]
         lib.fat_prefill_paged.restype = ctypes.c_int
@@ -290,10 +297,6 @@ def _load() -> None:
         lib.fat_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), _c_vp]
         lib.fat_append_kv.restype = ctypes.c_int
         lib.fat_append_kv.argtypes = [ctypes.POINTER(AppendArgs), _c_vp]
-        version = lib.fat_abi_version()
-        if version != ABI_VERSION:
-            _ERROR = f"{path} has ABI version {version}, expected {ABI_VERSION}; rebuild it"
-            return
         _LIB = lib
 
 
@@ -347,6 +350,11 @@ def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, split_k: i
 
 def prefill_workspace_bytes(total_k: int, num_kv_heads: int, head_dim: int) -> int:
     return int(lib().fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim))
+
+
+def prefill_varlen_workspace_bytes(a: PrefillArgs) -> int:
+    """Workspace bytes the launch of ``a`` uses (0: it runs without one)."""
+    return int(lib().fat_prefill_varlen_workspace_bytes(ctypes.byref(a)))
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -473,8 +481,12 @@ def prefill_varlen(
     """Enqueue ``fat_prefill_varlen`` for already-validated device tensors."""
     a = prefill_args(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k, causal,
                      softmax_scale, workspace=workspace, kernel=kernel)
-    handle = current_stream_handle(q.device) if stream is None else stream
-    _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(handle)), "fat_prefill_varlen")
+    prefill_varlen_with_args(a, current_stream_handle(q.device) if stream is None else stream)
+
+
+def prefill_varlen_with_args(a: PrefillArgs, stream: int) -> None:
+    """Enqueue ``fat_prefill_varlen`` from a filled argument block."""
+    _check(lib().fat_prefill_varlen(ctypes.byref(a), _c_vp(stream)), "fat_prefill_varlen")
 
 
 def prefill_args(

@@ -1204,6 +1204,16 @@ extern "C" int fat_paged_decode_noalloc(const fat_decode_args* a, void* stream) 
     fat_host::set_error("fat_paged_decode_noalloc: no current HIP device (or device id >= %d)", kMaxDevices);
     return FAT_E_INVALID;
   }
+  // The array is per device: a stream of another device would get this
+  // device's address and fault or corrupt there.
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess || sdev != dev) {
+      fat_host::set_error("fat_paged_decode_noalloc: the stream belongs to device %d, the current device is %d",
+                          (int)sdev, dev);
+      return FAT_E_INVALID;
+    }
+  }
   std::call_once(g_scratch_once[dev], [dev] {
     void* ptr = nullptr;
     g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));

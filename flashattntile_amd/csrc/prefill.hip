@@ -50,6 +50,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "fat_common.h"
@@ -74,7 +75,7 @@ struct PrefillParams {
   int32_t pshift;       // log2(page_size)
   int32_t num_pages, max_pages;
   // bf16 V converted ahead of the kernel (VPRE instantiations): v points at
-  // fp16 values scaled by 2^-v_head_scale[kv head].
+  // fp16 values scaled by 2^-v_head_scale[sequence * Hkv + kv head].
   const int32_t* v_head_scale;
 };
 
@@ -810,9 +811,9 @@ void prefill_pp_kernel(const PrefillParams p) {
   // <= 2^-25 * 2^s); vsc[buffer][wave] holds s.  The softmax folds
   // 2^(s - e_acc) into P's exponent, where O is kept as acc * 2^e_acc.
   constexpr bool VH = std::is_same<T, BF16>::value;
-  // VPRE: V arrives as fp16 already, scaled by one power of two per KV head
-  // (bf16v_to_f16_kernel), so staging is a plain copy and every wave's scale
-  // is the head's.
+  // VPRE: V arrives as fp16 already, scaled by one power of two per
+  // (sequence, KV head) (bf16v_to_f16_kernel), so staging is a plain copy and
+  // every wave's scale is that one.
   static_assert(!VPRE || (VH && PG == 0), "V pre-conversion is for packed bf16 prefill");
   __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
@@ -878,7 +879,7 @@ void prefill_pp_kernel(const PrefillParams p) {
   uint16_t* const lds0 = grp ? &Vs[0][0] : &Ks[0][0];
   const int lds_buf = grp ? kBN * V_RS : kBN * K_RS;
   const int lds_off = (gt / CPR) * lds_rs + 8 * (gt % CPR);
-  const int vpre_sw = VPRE ? p.v_head_scale[kvh] : 0;
+  const int vpre_sw = VPRE ? p.v_head_scale[b * p.Hkv + kvh] : 0;
   u32x4 stage[LOADS];
   // PAGED only: this group's K or V stream (PG 1 per-lane page ids, PG 2
   // wave-uniform ones).
@@ -1139,69 +1140,110 @@ void prefill_pp_kernel(const PrefillParams p) {
 // product is one fp16 MFMA with P rounded to fp16; bf16 V must therefore be
 // staged as fp16.  Converting it inside the kernel costs each group-B wave
 // ~80 VALU instructions per tile; converting it once beforehand costs one
-// read and one write of V.  One power of two per KV head keeps every value
-// inside fp16's range: 2^-s with s = 0 unless some |v| >= 2^15 (then s = the
-// head's largest exponent - 14).  Values are exact apart from fp16
-// subnormals (absolute error <= 2^-25 * 2^s), as in the in-kernel form.
+// read and one write of V.  One power of two per (sequence, KV head) keeps
+// every value inside fp16's range: 2^-s with s = 0 unless some finite |v| of
+// that sequence and head is >= 2^15 (then s = its largest exponent - 14).
+// Values are exact apart from fp16 subnormals (absolute error <= 2^-25 *
+// 2^s), as in the in-kernel form, and a sequence's scale depends on its own
+// rows only, so one sequence's magnitudes never reach another's results.
+// inf and NaN (exponent field 0xff) stay out of the maximum and convert to
+// fp16 inf and NaN.
+//
+// The pre-pass walks each sequence in 64-row tiles that start at the
+// sequence's first row.  Tile t of sequence b records its maximum in slot
+// b + floor(cu_k[b] / 64) + t of its head's row of `tilemax`: consecutive
+// sequences never share a slot, and every slot is below nblk + B (nblk =
+// ceil(total_k / 64)).
 // ---------------------------------------------------------------------------
-constexpr int kVpreRows = 64;  // V rows per pre-pass workgroup
+constexpr int kVpreRows = 64;  // V rows per pre-pass tile
 
-// Largest bf16 exponent field of |v| over rows [blk * 64, blk * 64 + 64) of
-// KV head h -> blockmax[h * nblk + blk].
-template <int D>
-__global__ __launch_bounds__(256) void bf16v_expmax_kernel(const uint16_t* __restrict__ v, int64_t v_st,
-                                                           int64_t v_sh, int total_k, int nblk,
-                                                           int32_t* __restrict__ blockmax) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  const int blk = blockIdx.x;
-  const int h = blockIdx.y;
-  u32 em = 0;
-  for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
-    const int row = blk * kVpreRows + c / CPR;
-    if (row < total_k) {
-      const u32x4 x = *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) em = max(em, max(x[e] & 0x7f80u, (x[e] >> 16) & 0x7f80u));
-    }
-  }
-  __shared__ u32 red[4];
-  u32 m = em;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = max(m, (u32)__shfl_xor((int)m, off));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) blockmax[h * nblk + blk] = (int32_t)(max(max(red[0], red[1]), max(red[2], red[3])) >> 7);
+// Rows [r0, r1) of sequence b (clamped into [0, total_k)) and its tile count.
+struct VpreSeq {
+  int r0, r1, ntiles, slot0;
+};
+__device__ __forceinline__ VpreSeq vpre_seq(const int32_t* __restrict__ cu_k, int b, int total_k, int nslot) {
+  VpreSeq s;
+  s.r0 = min(max(cu_k[b], 0), total_k);
+  s.r1 = min(max(cu_k[b + 1], s.r0), total_k);
+  s.ntiles = (s.r1 - s.r0 + kVpreRows - 1) / kVpreRows;
+  s.slot0 = b + s.r0 / kVpreRows;
+  s.ntiles = min(s.ntiles, max(nslot - s.slot0, 0));  // in range for any cu_k
+  return s;
 }
 
-// fp16(v * 2^-s_h) of rows [blk * 64, blk * 64 + 64) of KV head h into the
-// dense [total_k, Hkv, D] array v16; workgroup (0, h) records s_h.
+// Largest finite bf16 exponent field of |v| over tile t of sequence b, KV
+// head h -> tilemax[h * nslot + slot].  Grid (x, Hkv, B); workgroup x takes
+// tiles x, x + gridDim.x, ...
+template <int D>
+__global__ __launch_bounds__(256) void bf16v_expmax_kernel(const uint16_t* __restrict__ v, int64_t v_st,
+                                                           int64_t v_sh, const int32_t* __restrict__ cu_k,
+                                                           int total_k, int nslot,
+                                                           int32_t* __restrict__ tilemax) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const VpreSeq sq = vpre_seq(cu_k, b, total_k, nslot);
+  __shared__ u32 red[4];
+  for (int t = blockIdx.x; t < sq.ntiles; t += gridDim.x) {
+    u32 em = 0;
+    for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
+      const int row = sq.r0 + t * kVpreRows + c / CPR;
+      if (row < sq.r1) {
+        const u32x4 x =
+            *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const u32 lo = x[e] & 0x7f80u, hi = (x[e] >> 16) & 0x7f80u;
+          em = max(em, max(lo == 0x7f80u ? 0u : lo, hi == 0x7f80u ? 0u : hi));
+        }
+      }
+    }
+    u32 m = em;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (u32)__shfl_xor((int)m, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      tilemax[(int64_t)h * nslot + sq.slot0 + t] = (int32_t)(max(max(red[0], red[1]), max(red[2], red[3])) >> 7);
+    __syncthreads();
+  }
+}
+
+// fp16(v * 2^-s) of the tiles of sequence b, KV head h, into the dense
+// [total_k, Hkv, D] array v16, where s is the (b, h) scale taken from that
+// sequence's tile maxima; workgroup (0, h, b) records s in
+// seq_scale[b * Hkv + h] (0 for a sequence without keys).
 template <int D>
 __global__ __launch_bounds__(256) void bf16v_to_f16_kernel(const uint16_t* __restrict__ v, int64_t v_st, int64_t v_sh,
-                                                           int total_k, int Hkv, int nblk,
-                                                           const int32_t* __restrict__ blockmax,
-                                                           uint16_t* __restrict__ v16, int32_t* __restrict__ head_scale) {
+                                                           const int32_t* __restrict__ cu_k, int total_k, int Hkv,
+                                                           int nslot, const int32_t* __restrict__ tilemax,
+                                                           uint16_t* __restrict__ v16,
+                                                           int32_t* __restrict__ seq_scale) {
   constexpr int CPR = D / 8;
-  const int blk = blockIdx.x;
   const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const VpreSeq sq = vpre_seq(cu_k, b, total_k, nslot);
   int le = 0;
-  for (int i = threadIdx.x; i < nblk; i += 256) le = max(le, blockmax[h * nblk + i]);
+  for (int i = threadIdx.x; i < sq.ntiles; i += 256) le = max(le, tilemax[(int64_t)h * nslot + sq.slot0 + i]);
   __shared__ int red[4];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) le = max(le, __shfl_xor(le, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = le;
   __syncthreads();
   le = max(max(red[0], red[1]), max(red[2], red[3]));
-  const int sw = max(0, le - 141);  // 2^(le - 127) >= 2^15 <=> le >= 142
-  if (blk == 0 && threadIdx.x == 0) head_scale[h] = sw;
-  const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 128
-  for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
-    const int row = blk * kVpreRows + c / CPR;
-    if (row >= total_k) continue;
-    const u32x4 x = *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
-    u32x4 y;
+  const int sw = max(0, le - 141);  // 2^(le - 127) >= 2^15 <=> le >= 142; finite le <= 254
+  if (blockIdx.x == 0 && threadIdx.x == 0) seq_scale[b * Hkv + h] = sw;
+  const float f = as_f32((u32)(127 - sw) << 23);  // 2^-sw, sw <= 113
+  for (int t = blockIdx.x; t < sq.ntiles; t += gridDim.x) {
+    for (int c = threadIdx.x; c < kVpreRows * CPR; c += 256) {
+      const int row = sq.r0 + t * kVpreRows + c / CPR;
+      if (row >= sq.r1) continue;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(v + (int64_t)row * v_st + (int64_t)h * v_sh + 8 * (c % CPR));
+      u32x4 y;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = Pair<F16>::pack(Pair<BF16>::lo(x[e]) * f, Pair<BF16>::hi(x[e]) * f);
-    *reinterpret_cast<u32x4*>(v16 + ((int64_t)row * Hkv + h) * D + 8 * (c % CPR)) = y;
+      for (int e = 0; e < 4; ++e) y[e] = Pair<F16>::pack(Pair<BF16>::lo(x[e]) * f, Pair<BF16>::hi(x[e]) * f);
+      *reinterpret_cast<u32x4*>(v16 + ((int64_t)row * Hkv + h) * D + 8 * (c % CPR)) = y;
+    }
   }
 }
 
@@ -1305,11 +1347,9 @@ bool valid_prefill_kernel(int kernel) {
 // chains of at least FAT_PF_SPLIT_LONG tiles (the merge then costs less than
 // the balance gained).  A non-AUTO `kernel` argument forces one kernel (the
 // tests run every kernel on every shape that way).
-template <int PG>
-int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
-                   float softmax_scale, int kernel, const char* who, hipStream_t stream, void* workspace = nullptr,
-                   int total_k = 0, int total_q = 0) {
-  const int64_t heads = (int64_t)prm.B * prm.H;
+PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t max_seqlen_k, bool causal,
+                                int kernel, int D) {
+  const int64_t heads = B * H;
   const int64_t n_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM * heads;
   const int64_t n_4w = (max_seqlen_q + fat::kBM - 1) / fat::kBM * heads;
   const int64_t chain = (max_seqlen_k + fat::kBN - 1) / fat::kBN;
@@ -1323,11 +1363,42 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
            : kernel == FAT_KERNEL_PREFILL_4WAVE  ? PF_4WAVE
                                                  : PF_4WAVE_SPLIT;
   }
+  if (D == 256) kind = PF_4WAVE;  // see launch_prefill
+  return kind;
+}
+
+// Workspace bytes of the bf16 V pre-pass of a packed launch, or 0 when the
+// launch converts V in the kernel instead.  The pre-pass runs on the
+// ping-pong kernel when the sequences average at least kVpreMinMeanQ query
+// tokens (where the copy costs less than it saves: the pre-pass reads V twice
+// and writes it once, while the kernel converts each V tile once per (query
+// block, query head) that stages it; measured (bf16, 32/8 heads, D128): 3-6 %
+// faster from a mean of 2048 query tokens per sequence, level at 1024, 1-5 %
+// slower at 512), when the dense fp16 copy keeps the kernel's 32-bit
+// per-sequence offsets, and when the sequences average at least 32 keys
+// (2 B <= nblk + 1), which keeps the per-sequence scale arrays inside
+// fat_prefill_workspace_bytes.  Layout: the fp16 copy [total_k, Hkv, D]
+// (256-byte aligned), tile maxima [Hkv, nblk + B], scales [B, Hkv].
+size_t vpre_need(PrefillKind kind, int dtype, int64_t B, int64_t Hkv, int D, int64_t total_q, int64_t total_k,
+                 int64_t max_seqlen_k) {
+  if (dtype != FAT_DTYPE_BF16 || kind != PF_PINGPONG || D == 256 || total_k <= 0) return 0;
+  if (total_q < kVpreMinMeanQ * B) return 0;
+  if (max_seqlen_k * 2 * Hkv * D >= 0x7fffffffLL || 2 * Hkv * D >= (1 << 24)) return 0;
+  const int64_t nblk = (total_k + fat::kVpreRows - 1) / fat::kVpreRows;
+  if (2 * B > nblk + 1) return 0;
+  return vpre_bytes_v16(total_k, Hkv, D) + (size_t)(Hkv * (nblk + 2 * B)) * sizeof(int32_t);
+}
+
+template <int PG>
+int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
+                   float softmax_scale, int kernel, const char* who, hipStream_t stream, void* workspace = nullptr,
+                   int total_k = 0, int total_q = 0) {
+  PrefillKind kind = choose_prefill_kind(prm.B, prm.H, max_seqlen_q, max_seqlen_k, causal, kernel, D);
   // head_dim 256: O and Q alone take 192 registers per lane, so only the
   // 4-wave kernel (one wave per SIMD) runs it; its K/V tiles take 141 KB of
   // LDS, which leaves no room for the split's second group.
   if (D == 256) {
-    if (kernel != FAT_KERNEL_AUTO && kind != PF_4WAVE) {
+    if (kernel != FAT_KERNEL_AUTO && kernel != FAT_KERNEL_PREFILL_4WAVE) {
       fat_host::set_error("%s: head_dim 256 runs on the 4-wave prefill kernel only (kernel %d)", who, kernel);
       return FAT_E_UNSUPPORTED;
     }
@@ -1342,47 +1413,45 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     return FAT_E_UNSUPPORTED;
   }
   const dim3 grid((unsigned)n);
-  // Packed bf16 on the ping-pong kernel: convert V to fp16 first when the
-  // caller gave the workspace (and the dense fp16 copy keeps the kernel's
-  // 32-bit per-sequence offsets), and when V tiles are staged often enough
-  // for the copy to pay: the pre-pass reads V twice and writes it once, while
-  // the kernel converts each V tile once per (query block, query head) that
-  // stages it.  Measured (bf16, 32/8 heads, D128): 3-6 % faster from a mean
-  // of 2048 query tokens per sequence, level at 1024, 1-5 % slower at 512
-  // (5 % for 512-token chunks after a 3584-token prefix).
+  // Packed bf16 on the ping-pong kernel: convert V to fp16 first (vpre_need)
+  // when the caller gave the workspace.
   prm.v_head_scale = nullptr;
-  if (PG == 0 && dtype == FAT_DTYPE_BF16 && kind == PF_PINGPONG && workspace && total_k > 0 &&
-      (int64_t)total_q >= kVpreMinMeanQ * (int64_t)prm.B &&
-      (int64_t)max_seqlen_k * 2 * prm.Hkv * D < 0x7fffffffLL && 2 * prm.Hkv * D < (1 << 24)) {
+  if (PG == 0 && workspace && vpre_need(kind, dtype, prm.B, prm.Hkv, D, total_q, total_k, max_seqlen_k) > 0) {
     const int nblk = (total_k + fat::kVpreRows - 1) / fat::kVpreRows;
+    const int nslot = nblk + prm.B;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     uint16_t* v16 = reinterpret_cast<uint16_t*>(ws);
-    int32_t* blockmax = reinterpret_cast<int32_t*>(ws + vpre_bytes_v16(total_k, prm.Hkv, D));
-    int32_t* head_scale = blockmax + (int64_t)prm.Hkv * nblk;
-    const dim3 pgrid((unsigned)nblk, (unsigned)prm.Hkv);
+    int32_t* tilemax = reinterpret_cast<int32_t*>(ws + vpre_bytes_v16(total_k, prm.Hkv, D));
+    int32_t* seq_scale = tilemax + (int64_t)prm.Hkv * nslot;
+    // One workgroup per tile of the longest sequence (max_seqlen_k bounds the
+    // tile count; a workgroup loops over the tiles beyond gridDim.x anyway).
+    const int64_t tiles = (max_seqlen_k + fat::kVpreRows - 1) / fat::kVpreRows;
+    const dim3 pgrid((unsigned)std::max<int64_t>(1, std::min<int64_t>(tiles, 65535)), (unsigned)prm.Hkv,
+                     (unsigned)prm.B);
     const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(prm.v);
+    const int32_t* cuk = prm.cu_k;
     if (D == 128) {
       hipLaunchKernelGGL((fat::bf16v_expmax_kernel<128>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, nblk, blockmax);
+                         cuk, total_k, nslot, tilemax);
       hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<128>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+                         cuk, total_k, prm.Hkv, nslot, tilemax, v16, seq_scale);
     } else if (D == 64) {
       hipLaunchKernelGGL((fat::bf16v_expmax_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, nblk, blockmax);
+                         cuk, total_k, nslot, tilemax);
       hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<64>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+                         cuk, total_k, prm.Hkv, nslot, tilemax, v16, seq_scale);
     } else {
       hipLaunchKernelGGL((fat::bf16v_expmax_kernel<32>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, nblk, blockmax);
+                         cuk, total_k, nslot, tilemax);
       hipLaunchKernelGGL((fat::bf16v_to_f16_kernel<32>), pgrid, dim3(256), 0, stream, vsrc, prm.v_st, prm.v_sh,
-                         total_k, prm.Hkv, nblk, blockmax, v16, head_scale);
+                         cuk, total_k, prm.Hkv, nslot, tilemax, v16, seq_scale);
     }
     const int rc = fat_host::launch_status("bf16v_to_f16_kernel");
     if (rc != FAT_OK) return rc;
     prm.v = reinterpret_cast<const uint8_t*>(v16);
     prm.v_st = (int64_t)prm.Hkv * D;
     prm.v_sh = D;
-    prm.v_head_scale = head_scale;
+    prm.v_head_scale = seq_scale;
   }
   if (dtype == FAT_DTYPE_F16) return launch_prefill_d<fat::F16, PG>(prm, D, causal, kind, grid, stream);
   return launch_prefill_d<fat::BF16, PG>(prm, D, causal, kind, grid, stream);
@@ -1393,7 +1462,17 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
 extern "C" size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads, int32_t head_dim) {
   if (total_k <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
   const size_t nblk = ((size_t)total_k + fat::kVpreRows - 1) / fat::kVpreRows;
-  return vpre_bytes_v16(total_k, num_kv_heads, head_dim) + (nblk + 1) * (size_t)num_kv_heads * sizeof(int32_t);
+  return vpre_bytes_v16(total_k, num_kv_heads, head_dim) + (2 * nblk + 1) * (size_t)num_kv_heads * sizeof(int32_t);
+}
+
+extern "C" size_t fat_prefill_varlen_workspace_bytes(const fat_prefill_args* a) {
+  if (!a || a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->total_q <= 0 || a->total_k <= 0 ||
+      a->max_seqlen_q <= 0 || a->max_seqlen_k < 0 || !valid_prefill_kernel(a->kernel))
+    return 0;
+  const PrefillKind kind = choose_prefill_kind(a->batch, a->num_heads, a->max_seqlen_q, a->max_seqlen_k,
+                                               a->causal != 0, a->kernel, a->head_dim);
+  return vpre_need(kind, a->dtype, a->batch, a->num_kv_heads, a->head_dim, a->total_q, a->total_k,
+                   a->max_seqlen_k);
 }
 
 extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {

@@ -101,12 +101,15 @@ def _validate_inputs(q, k, v, cu_seqlens_q, cu_seqlens_k, causal) -> tuple[int, 
     ck = cu_seqlens_k.to(torch.int64)
     lq = cq[1:] - cq[:-1]
     lk = ck[1:] - ck[:-1]
+    keyless = (lk == 0) & (lq > 0)
+    first_keyless = keyless.to(torch.int64).argmax()
     stats = torch.stack([
         cq[0], ck[0], cq[-1], ck[-1],
         (lq < 0).any().to(torch.int64), (lk < 0).any().to(torch.int64),
         (lk < lq).any().to(torch.int64), lq.max(), lk.max(),
+        keyless.any().to(torch.int64), first_keyless, lq[first_keyless],
     ]).cpu().tolist()
-    q0, k0, q_end, k_end, q_dec, k_dec, short_kv, max_q, max_k = (int(x) for x in stats)
+    q0, k0, q_end, k_end, q_dec, k_dec, short_kv, max_q, max_k, any_keyless, kl_b, kl_q = (int(x) for x in stats)
     if q0 != 0 or k0 != 0:
         raise ValueError("cu_seqlens must start at 0")
     if q_end != q.shape[0]:
@@ -119,6 +122,8 @@ def _validate_inputs(q, k, v, cu_seqlens_q, cu_seqlens_k, causal) -> tuple[int, 
         raise ValueError("cu_seqlens_k must be non-decreasing")
     if causal and short_kv:
         raise ValueError("causal bottom-right alignment requires kv_len >= q_len per sequence")
+    if any_keyless:  # reference.py:115-116 (the kernels would write zeros)
+        raise ValueError(f"sequence {kl_b} has {kl_q} queries but no keys")
     if q.shape[1] % k.shape[1] != 0:
         raise ValueError(f"num_heads ({q.shape[1]}) must be divisible by num_kv_heads ({k.shape[1]})")
     return max_q, max_k
@@ -148,16 +153,20 @@ def prefill_launch(
         raise ValueError("q, k, v need a contiguous head_dim axis")
     if out is None:
         out = torch.empty_like(q)
-    # bf16 takes a workspace for the fp16 copy of V the large-grid kernel
-    # stages (fp16 needs none); without one the kernel converts V itself.
-    need = _hip.prefill_workspace_bytes(k.shape[0], k.shape[1], k.shape[2]) if q.dtype == torch.bfloat16 else 0
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     # The kernels read cu_seqlens densely.
     cu_seqlens_q = cu_seqlens_q if cu_seqlens_q.is_contiguous() else cu_seqlens_q.contiguous()
     cu_seqlens_k = cu_seqlens_k if cu_seqlens_k.is_contiguous() else cu_seqlens_k.contiguous()
-    _hip.prefill_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k,
-                        causal, softmax_scale, workspace=workspace, kernel=_KERNEL_CODES[kernel])
+    a = _hip.prefill_args(q, k, v, cu_seqlens_q, cu_seqlens_k, out, max_seqlen_q, max_seqlen_k, causal,
+                          softmax_scale, workspace=None, kernel=_KERNEL_CODES[kernel])
+    # Long bf16 launches on the large-grid kernel stage an fp16 copy of V from
+    # a workspace; the library says how much this launch uses (0 for fp16 and
+    # every other launch), so nothing is allocated that it would not use.
+    need = _hip.prefill_varlen_workspace_bytes(a)
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        a.workspace = workspace.data_ptr()
+    _hip.prefill_varlen_with_args(a, _hip.current_stream_handle(q.device))
     return out
 
 
@@ -242,11 +251,13 @@ def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
     big, small = torch.iinfo(torch.int32).max, torch.iinfo(torch.int32).min
     lo = torch.where(used, pt, torch.full_like(pt, big)).min().to(torch.int64) if pt.numel() else sl.max() * 0
     hi = torch.where(used, pt, torch.full_like(pt, small)).max().to(torch.int64) if pt.numel() else sl.max() * 0
+    keyless = (sl <= 0) & (lq > 0)
+    first_keyless = keyless.to(torch.int64).argmax()
     stats = torch.stack([
         cq[0], cq[-1], (lq < 0).any().to(torch.int64), lq.max(), (sl < lq).any().to(torch.int64),
-        sl.min(), sl.max(), lo, hi,
+        sl.min(), sl.max(), lo, hi, keyless.any().to(torch.int64), first_keyless, lq[first_keyless],
     ]).cpu().tolist()
-    q0, q_end, q_dec, max_q, short_kv, min_len, max_len, lo, hi = (int(x) for x in stats)
+    q0, q_end, q_dec, max_q, short_kv, min_len, max_len, lo, hi, any_keyless, kl_b, kl_q = (int(x) for x in stats)
     if q0 != 0:
         raise ValueError("cu_seqlens must start at 0")
     if q_end != q.shape[0]:
@@ -264,6 +275,8 @@ def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
             raise AssertionError(f"page_table references page {hi} but cache has {cache.num_pages} pages")
     if causal and short_kv:
         raise ValueError("causal bottom-right alignment requires kv_len >= q_len per sequence")
+    if any_keyless:  # reference.py:115-116, as for packed prefill
+        raise ValueError(f"sequence {kl_b} has {kl_q} queries but no keys")
     return max_q
 
 

@@ -43,13 +43,15 @@
 extern "C" {
 #endif
 
-/* 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
+/* 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
+ *     the bf16 V pre-pass scales V per (sequence, KV head).
+ * 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
  *     uses the workspace for an fp16 copy of V (optional).
  * 9: fat_paged_decode_noalloc (allocation-free decode).
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 10
+#define FAT_ABI_VERSION 11
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -188,14 +190,15 @@ typedef struct fat_decode_args {
  * FAT_E_UNSUPPORTED).  The same holds for fat_prefill_paged.
  * Causal masking is bottom-right aligned: query i of a sequence sees key j
  * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
- * `workspace` is optional (NULL, or 256-byte aligned and holding
- * fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim) bytes).
- * fp16 ignores it.  With bf16 the large-grid kernel then stages an fp16
- * copy of V written there by a pre-pass (one power-of-two scale per KV
- * head; results within the same bound as the in-kernel conversion it
- * replaces) when the sequences average at least 2048 query tokens, where
- * the copy costs less than it saves; otherwise, or without the workspace,
- * the kernel converts V tile by tile.
+ * `workspace` is optional: NULL, or 256-byte aligned and holding
+ * fat_prefill_varlen_workspace_bytes(args) bytes (at most
+ * fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim)).  Only bf16
+ * launches on the large-grid kernel whose sequences average at least 2048
+ * query tokens use it (the query returns 0 otherwise): a pre-pass writes an
+ * fp16 copy of V there, scaled by one power of two per (sequence, KV head),
+ * and the kernel stages that copy (results within the same bound as the
+ * in-kernel conversion it replaces).  Without the workspace the kernel
+ * converts V tile by tile.
  */
 typedef struct fat_prefill_args {
   const void* q;
@@ -367,13 +370,26 @@ int fat_paged_decode(const fat_decode_args* args, void* stream);
  * (fat_paged_decode_workspace_bytes of its batch * q_len rows) exceeds the
  * maximum returns FAT_E_INVALID.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (e.g. on two streams) race.  The
- * current HIP device must be the one `stream` belongs to. */
+ * current HIP device must be the one `stream` belongs to (FAT_E_INVALID
+ * otherwise).  The first call on a device looks up the array's address
+ * (hipGetSymbolAddress); make it before capturing the call in a HIP graph,
+ * as a warm-up launch before capture does.  Replays of a captured call reuse
+ * the same array. */
 #define FAT_DECODE_NOALLOC_MAX_WORKSPACE ((size_t)32 << 20)
 int fat_paged_decode_noalloc(const fat_decode_args* args, void* stream);
 
-/* Bytes of the optional fat_prefill_varlen workspace (used by bf16). */
+/* Upper bound on the optional fat_prefill_varlen workspace of any launch
+ * with these K/V sizes (used by bf16 only). */
 size_t fat_prefill_workspace_bytes(int32_t total_k, int32_t num_kv_heads,
                                    int32_t head_dim);
+
+/* Bytes of workspace the launch described by `args` would use: 0 when it
+ * runs without one (fp16, short sequences, the small-grid kernels).  Reads
+ * only the sizes, dtype, causal and kernel fields; no device access, so a
+ * caller can size the buffer before any allocation or graph capture.
+ * No reference counterpart: the reference's prefill allocates nothing
+ * besides its output (flashattn_tile/kernels/prefill.py:295). */
+size_t fat_prefill_varlen_workspace_bytes(const fat_prefill_args* args);
 
 /* Enqueue varlen prefill on `stream`.
  * Replaces flashattn_tile/kernels/prefill.py:236-326 (see file header). */

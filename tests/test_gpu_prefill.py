@@ -51,6 +51,54 @@ def test_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
     assert_parity(out, _ref32(q, k, v, cu, cu, causal), label=label)
 
 
+# (kv_len, q_len) per sequence: entries with no queries, with and without
+# keys, at both ends and between sequences that have work (a serving batch
+# where some sequences have no new tokens this step).
+EMPTY_Q = [(0, 0), (40, 0), (17, 17), (0, 0), (300, 300), (129, 0), (64, 1), (700, 513), (9, 0)]
+
+
+def _varlen_kq(pairs, h, hk, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    lk = [p[0] for p in pairs]
+    lq = [p[1] for p in pairs]
+
+    def offsets(lens):
+        return torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32, device=DEV)
+
+    q = torch.randn(sum(lq), h, d, generator=g).to(dtype).to(DEV)
+    k = torch.randn(sum(lk), hk, d, generator=g).to(dtype).to(DEV)
+    v = torch.randn(sum(lk), hk, d, generator=g).to(dtype).to(DEV)
+    return q, k, v, offsets(lq), offsets(lk), max(lq), max(lk)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_batch_with_sequences_without_queries(dtype, causal, kernel):
+    """q_len = 0 sequences take the kernels' early return and leave the
+    other sequences' results unchanged: parity for the whole batch, and
+    bit-identity, on a forced kernel, with the same batch without them."""
+    label = f"prefill {kernel} {dtype} empty-query entries causal={causal}"
+    print(label, flush=True)
+    q, k, v, cq, ck, mq, mk = _varlen_kq(EMPTY_Q, 16, 4, 128, dtype, seed=41)
+    out = prefill_attention(q, k, v, cq, ck, mq, mk, causal=causal)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, k, v, cq, ck, causal), label=label)
+    if kernel == "auto":  # the smaller batch may get another kernel
+        return
+    # The same work without the empty entries on the same kernel: identical bits.
+    keep = [i for i, (_, n) in enumerate(EMPTY_Q) if n > 0]
+    kst, qst = ck.tolist(), cq.tolist()
+    k2 = torch.cat([k[kst[i]:kst[i + 1]] for i in keep])
+    v2 = torch.cat([v[kst[i]:kst[i + 1]] for i in keep])
+    lens_k = [EMPTY_Q[i][0] for i in keep]
+    lens_q = [EMPTY_Q[i][1] for i in keep]
+    ck2 = torch.tensor([0] + torch.cumsum(torch.tensor(lens_k), 0).tolist(), dtype=torch.int32, device=DEV)
+    cq2 = torch.tensor([0] + torch.cumsum(torch.tensor(lens_q), 0).tolist(), dtype=torch.int32, device=DEV)
+    out2 = prefill_attention(q, k2, v2, cq2, ck2, mq, max(lens_k), causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), label
+
+
 # head_dim 32 runs on every prefill kernel; head_dim 256 on the 4-wave kernel
 # only (O and Q take 192 registers per lane), which the others refuse.
 HEAD_DIM_KERNELS = {32: [None, "pingpong", "4wave", "4wave_split"], 256: [None, "4wave"]}
@@ -252,7 +300,7 @@ def test_prefill_bf16_v_beyond_fp16_range(huge, kernel):
 
 def test_prefill_bf16_with_and_without_workspace():
     """bf16 on the ping-pong kernel with the workspace (V converted to fp16
-    by the pre-pass, one scale per KV head) and without it (V converted tile
+    by the pre-pass, one scale per sequence and KV head) and without it (V converted tile
     by tile in the kernel): bit-identical while every |v| < 2^15 (both scales
     are 1), and both within the tolerance when a row reaches 1e6.  The
     sequence has the 2048 queries from which the library runs the pre-pass."""
@@ -283,3 +331,50 @@ def test_prefill_bf16_with_and_without_workspace():
             excess = ((o32 - r32).abs() - rounding) / scale
             print(f"kv{kvh} {name}: max relative error beyond rounding {excess.max().item():.3e}", flush=True)
             assert torch.isfinite(o32).all() and excess.max().item() <= 2e-3, (kvh, name)
+
+
+def test_prefill_bf16_prepass_keeps_sequences_independent():
+    """The bf16 V pre-pass scales V per (sequence, KV head): a V row of 1e12
+    in one sequence and inf in another leave the other sequences of the same
+    packed launch at parity with the oracle and bit-identical to the launch
+    without a workspace (in-kernel conversion, scale 1 on clean tiles), and
+    the inf still reaches the queries of its own sequence that see it."""
+    from flashattntile_amd import _hip
+
+    lens = [2304, 2560, 2432, 2048]  # a mean of >= 2048 queries: the pre-pass runs
+    H, HKV, D = 32, 8, 128
+    q, k, v, cu = make_varlen(lens, H, HKV, D, torch.bfloat16, seed=37, device=DEV)
+    starts = cu.tolist()
+    huge_row, inf_row = starts[1] + 900, starts[2] + 1500
+    v[huge_row, 2, 5] = 1.0e12
+    v[inf_row, 2, 7] = float("inf")
+    v[inf_row, 5, 0] = float("-inf")
+    L = max(lens)
+    out = torch.empty_like(q)
+    a = _hip.prefill_args(q, k, v, cu, cu, out, L, L, True, D ** -0.5, kernel=_hip.KERNEL_PREFILL_PINGPONG)
+    need = _hip.prefill_varlen_workspace_bytes(a)
+    print(f"prefill bf16 pre-pass isolation: workspace {need} B", flush=True)
+    assert 0 < need <= _hip.prefill_workspace_bytes(k.shape[0], HKV, D)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    a.workspace = ws.data_ptr()
+    _hip.prefill_varlen_with_args(a, _hip.current_stream_handle(q.device))
+    no_ws = torch.empty_like(q)
+    _hip.prefill_varlen(q, k, v, cu, cu, no_ws, L, L, True, D ** -0.5, workspace=None,
+                        kernel=_hip.KERNEL_PREFILL_PINGPONG)
+    torch.cuda.synchronize()
+    for b in (0, 3):
+        rows = slice(starts[b], starts[b + 1])
+        assert torch.equal(out[rows], no_ws[rows]), f"clean sequence {b}: pre-pass and in-kernel differ"
+        cu1 = torch.tensor([0, lens[b]], dtype=torch.int32)
+        for kvh in (2, 5, 0):
+            hs = slice(kvh * (H // HKV), (kvh + 1) * (H // HKV))
+            qs = q[rows, hs].contiguous().cpu()
+            ref = _ref32(qs, k[rows, kvh:kvh + 1].contiguous(), v[rows, kvh:kvh + 1].contiguous(), cu1, cu1, True)
+            assert_parity(out[rows, hs], ref, label=f"pre-pass isolation: clean sequence {b}, KV head {kvh}")
+    # Sequence 2's queries that see its inf key (causal: query i sees key j
+    # iff j <= i) have a non-finite output in the inf's column, in every head
+    # of that KV head, as the oracle's have.
+    seen = slice(inf_row, starts[3])
+    for kvh, col in ((2, 7), (5, 0)):
+        hs = slice(kvh * (H // HKV), (kvh + 1) * (H // HKV))
+        assert not torch.isfinite(out[seen, hs, col].float()).any(), kvh

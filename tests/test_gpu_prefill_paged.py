@@ -66,6 +66,37 @@ def test_paged_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
     assert_parity(out, _ref32(q, cache, cu, causal), label=label)
 
 
+# (kv_len, q_len): sequences with no new tokens this step (q_len = 0), with
+# cached keys or none, around sequences that prefill a chunk.
+IDLE_CHUNKS = [(1000, 0), (300, 77), (129, 0), (0, 0), (64, 64), (517, 0), (5, 3), (40, 0)]
+
+
+@pytest.mark.parametrize("P", [1, 16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paged_prefill_batch_with_idle_sequences(dtype, causal, P, kernel):
+    """A paged batch in which some sequences have no new tokens: parity, and
+    the working rows bit-identical, on a forced kernel, to a batch of only those."""
+    label = f"paged prefill {kernel} {dtype} P{P} idle sequences causal={causal}"
+    print(label, flush=True)
+    lens_k = [c[0] for c in IDLE_CHUNKS]
+    lens_q = [c[1] for c in IDLE_CHUNKS]
+    q, cache, cu = _case(lens_k, lens_q, 16, 4, 128, P, dtype, seed=53 + P)
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=causal)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache, cu, causal), label=label)
+    if kernel == "auto":  # the smaller batch may get another kernel
+        return
+    keep = [i for i, n in enumerate(lens_q) if n > 0]
+    sub = PagedKVCache(cache.k_cache, cache.v_cache, cache.page_table[keep].contiguous(),
+                       cache.seq_lens[keep].contiguous(), P)
+    cu2 = torch.tensor([0] + torch.cumsum(torch.tensor([lens_q[i] for i in keep]), 0).tolist(), dtype=torch.int32,
+                       device=DEV)
+    out2 = paged_prefill_attention(q, sub, cu2, max(lens_q), causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), label
+
+
 @pytest.mark.parametrize("P", [4, 16, 64])
 @pytest.mark.parametrize("d", [32, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -9,7 +9,7 @@ import torch
 import flashattntile_amd as fat
 from flashattntile_amd.backend import AttentionMetadata, FlashAttnTileBackend
 from flashattntile_amd.ops import PAGED_DECODE_OP, PAGED_DECODE_QUANT_OP, PREFILL_OP, ops_available
-from flashattntile_amd.paging import allocate, append_tokens
+from flashattntile_amd.paging import PagedKVCache
 
 SCHEMAS = {
     "paged_decode": "flashattn_tile::paged_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor page_table, "
@@ -20,12 +20,18 @@ SCHEMAS = {
 }
 
 
-def _cache(batch=2, length=12, page_size=16, kv_heads=2, head_dim=8, dtype=torch.float32, device="cpu"):
-    cache = allocate(batch, length, kv_heads, head_dim, page_size, dtype=dtype, device=device)
-    for _ in range(length):
-        append_tokens(cache, torch.randn(batch, kv_heads, head_dim).to(dtype).to(device),
-                      torch.randn(batch, kv_heads, head_dim).to(dtype).to(device))
-    return cache
+def _cache(lens=(12, 12), page_size=16, kv_heads=2, head_dim=8, dtype=torch.float32, seed=3) -> PagedKVCache:
+    """Host cache with identity page order, filled with seeded N(0,1) rows."""
+    g = torch.Generator().manual_seed(seed)
+    per = [-(-n // page_size) for n in lens]
+    shape = (sum(per), page_size, kv_heads, head_dim)
+    table = torch.zeros(len(lens), max(per), dtype=torch.int32)
+    at = 0
+    for b, n in enumerate(per):
+        table[b, :n] = torch.arange(at, at + n, dtype=torch.int32)
+        at += n
+    return PagedKVCache(torch.randn(shape, generator=g).to(dtype), torch.randn(shape, generator=g).to(dtype), table,
+                        torch.tensor(lens, dtype=torch.int32), page_size)
 
 
 def test_custom_ops_registered_with_reference_schemas():
@@ -37,27 +43,43 @@ def test_custom_ops_registered_with_reference_schemas():
     assert PAGED_DECODE_QUANT_OP in str(torch.ops.flashattn_tile.paged_decode_quant._schemas)
 
 
-def test_fake_paged_decode_shapes():
-    with torch._subclasses.fake_tensor.FakeTensorMode():
-        q = torch.empty(3, 4, 8, device="meta")
-        k = torch.empty(12, 16, 2, 8, device="meta")
-        pt = torch.empty(3, 3, dtype=torch.int32, device="meta")
-        sl = torch.full((3,), 5, dtype=torch.int32, device="meta")
-        out = torch.ops.flashattn_tile.paged_decode(q, k, k, pt, sl, 16, 0.35, 1)
-        sc = torch.empty(12, 2, device="meta")
-        outq = torch.ops.flashattn_tile.paged_decode_quant(q, k.to(torch.int8), k.to(torch.int8), sc, sc, pt, sl,
-                                                            16, 0.35, 2)
-    assert out.shape == (3, 4, 8) and out.dtype == torch.float32 and out.device.type == "meta"
-    assert outq.shape == (3, 4, 8)
+# (batch, q heads, kv heads, head_dim, pages, page_size, dtype) of the meta
+# problems the fake kernels are traced on.
+FAKE_DECODE_SHAPES = [
+    (1, 2, 1, 64, 5, 8, torch.float16),
+    (5, 12, 4, 32, 40, 32, torch.bfloat16),
+    (2, 16, 16, 128, 9, 1, torch.float32),
+]
 
 
-def test_fake_prefill_varlen_shapes():
+@pytest.mark.parametrize("b,h,hk,d,pages,ps,dtype", FAKE_DECODE_SHAPES)
+def test_fake_decode_ops_give_the_query_shape_and_dtype(b, h, hk, d, pages, ps, dtype):
+    """Under FakeTensorMode no kernel runs: both decode ops report an output
+    of the query's shape, dtype and device (kernels/decode.py's register_fake
+    contract, flashattn_tile/ops.py:56-73)."""
     with torch._subclasses.fake_tensor.FakeTensorMode():
-        q = torch.empty(11, 4, 8, device="meta")
-        k = torch.empty(11, 2, 8, device="meta")
-        cu = torch.full((3,), 0, dtype=torch.int32, device="meta")
-        out = torch.ops.flashattn_tile.prefill_varlen(q, k, k, cu, cu, 7, 7, True, 0.35)
-    assert out.shape == (11, 4, 8) and out.device.type == "meta"
+        q = torch.empty(b, h, d, dtype=dtype, device="meta")
+        kv = torch.empty(pages, ps, hk, d, dtype=dtype, device="meta")
+        table = torch.empty(b, pages, dtype=torch.int32, device="meta")
+        lens = torch.empty(b, dtype=torch.int32, device="meta")
+        scales = torch.empty(pages, hk, device="meta")
+        outs = [torch.ops.flashattn_tile.paged_decode(q, kv, kv, table, lens, ps, 0.125, 2)]
+        if dtype != torch.float32:
+            codes = kv.to(torch.float8_e4m3fn)
+            outs.append(torch.ops.flashattn_tile.paged_decode_quant(q, codes, codes, scales, scales, table, lens, ps,
+                                                                     0.125, 1))
+    for out in outs:
+        assert (tuple(out.shape), out.dtype, out.device.type) == ((b, h, d), dtype, "meta")
+
+
+@pytest.mark.parametrize("tokens,h,hk,d,dtype", [(1, 4, 4, 64, torch.float16), (37, 24, 8, 128, torch.bfloat16)])
+def test_fake_prefill_op_gives_the_query_shape_and_dtype(tokens, h, hk, d, dtype):
+    with torch._subclasses.fake_tensor.FakeTensorMode():
+        q = torch.empty(tokens, h, d, dtype=dtype, device="meta")
+        kv = torch.empty(tokens + 3, hk, d, dtype=dtype, device="meta")
+        cq = torch.empty(4, dtype=torch.int32, device="meta")
+        out = torch.ops.flashattn_tile.prefill_varlen(q, kv, kv, cq, cq, tokens, tokens + 3, False, 0.25)
+    assert (tuple(out.shape), out.dtype, out.device.type) == ((tokens, h, d), dtype, "meta")
 
 
 def test_fake_prefill_paged_shapes():
@@ -134,7 +156,7 @@ def test_cpu_tensors_raise_instead_of_falling_back():
     cu = torch.tensor([0, 3, 9], dtype=torch.int32)
     with pytest.raises(RuntimeError, match="ROCm device"):
         fat.prefill_attention(qp, kp, kp, cu, cu, max(lens), max(lens))
-    cache2 = _cache(batch=2, length=6, dtype=torch.float16)
+    cache2 = _cache(lens=(6, 6), dtype=torch.float16)
     with pytest.raises(RuntimeError, match="ROCm device"):
         fat.paged_prefill_attention(qp, cache2, cu, 6)
     with pytest.raises(RuntimeError, match="ROCm device"):
@@ -143,14 +165,22 @@ def test_cpu_tensors_raise_instead_of_falling_back():
         fat.AppendLaunch(cache)
 
 
-def test_backend_kv_cache_shape_matches_allocate():
-    backend = FlashAttnTileBackend(num_heads=8, num_kv_heads=2, head_dim=16, page_size=16)
-    cache = backend.allocate_kv_cache(batch=2, max_seq_len=160, dtype=torch.float32, device="cpu")
-    shape = backend.get_kv_cache_shape(num_blocks=cache.num_pages, block_size=16, num_kv_heads=2, head_dim=16)
-    assert shape == (2, cache.num_pages, 16, 2, 16)
-    assert shape[1:] == cache.k_cache.shape
-    assert backend.get_kv_cache_shape_per_tensor(cache.num_pages, 16, 2, 16) == cache.k_cache.shape
-    assert backend.get_name() == "flashattn_tile"
+@pytest.mark.parametrize("hk,d,ps,batch,max_len", [(1, 64, 32, 3, 70), (4, 128, 8, 1, 8), (8, 32, 1, 2, 5)])
+def test_backend_cache_shape_agrees_with_its_allocation(hk, d, ps, batch, max_len):
+    """The vLLM-style 5-D shape is (K and V, blocks, block_size, kv heads,
+    head_dim), and the cache the backend allocates is exactly one of its two
+    halves (flashattn_tile/backend.py:57-60, paging.py:30-60)."""
+    backend = FlashAttnTileBackend(num_heads=2 * hk, num_kv_heads=hk, head_dim=d, page_size=ps)
+    cache = backend.allocate_kv_cache(batch=batch, max_seq_len=max_len, dtype=torch.bfloat16, device="cpu")
+    assert cache.num_pages >= batch * -(-max_len // ps)
+    five = backend.get_kv_cache_shape(cache.num_pages, ps, hk, d)
+    assert five[0] == 2 and five[1:] == tuple(cache.v_cache.shape) == tuple(cache.k_cache.shape)
+    assert backend.get_kv_cache_shape_per_tensor(cache.num_pages, ps, hk, d) == five[1:]
+    assert FlashAttnTileBackend.get_kv_cache_shape(7, 4, 3, 2) == (2, 7, 4, 3, 2)
+
+
+def test_backend_reports_its_name():
+    assert FlashAttnTileBackend(num_heads=1, num_kv_heads=1, head_dim=32, page_size=4).get_name() == "flashattn_tile"
 
 
 def test_backend_validation_and_routing_errors():
@@ -186,13 +216,24 @@ def test_backend_validation_and_routing_errors():
         backend.forward(torch.randn(2, 3, 5, 8), cache, AttentionMetadata())
 
 
-def test_native_availability_is_graceful():
+def test_native_probe_never_raises_and_explains_itself():
+    """is_available() / unavailable_reason() are total (flashattn_tile/
+    native.py:54-84): the reason is empty exactly when the path is usable."""
     from flashattntile_amd import native
 
-    if torch.cuda.is_available():
-        assert native.is_available() or native.unavailable_reason()
-    else:
-        assert not native.is_available()
-        assert native.unavailable_reason()
-        with pytest.raises(RuntimeError, match="unavailable"):
-            native.paged_decode_attention(torch.zeros(1, 1, 8), None, None, None, None, 16)
+    usable = native.is_available()
+    reason = native.unavailable_reason()
+    assert isinstance(usable, bool) and isinstance(reason, str)
+    assert usable == (reason == "")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the host without a ROCm device")
+def test_native_decode_without_a_device_raises_with_the_reason():
+    from flashattntile_amd import native
+
+    assert not native.is_available()
+    cache = _cache(lens=(3,), head_dim=64)
+    with pytest.raises(RuntimeError, match="unavailable") as info:
+        native.paged_decode_attention(torch.zeros(1, 4, 64), cache.k_cache, cache.v_cache, cache.page_table,
+                                      cache.seq_lens, 16)
+    assert native.unavailable_reason() in str(info.value)
