@@ -984,7 +984,8 @@ def all_configs(args, device):
 PROFILE_SOURCES = {
     "decode": ["flashattntile_amd/csrc/decode.hip", "flashattntile_amd/csrc/decode_params.h",
                "flashattntile_amd/csrc/fat_common.h"],
-    "prefill": ["flashattntile_amd/csrc/prefill.hip", "flashattntile_amd/csrc/fat_common.h"],
+    "prefill": ["flashattntile_amd/csrc/prefill.hip", "flashattntile_amd/csrc/prefill_wide.hip",
+                "flashattntile_amd/csrc/prefill_common.h", "flashattntile_amd/csrc/fat_common.h"],
     "kvwrite": ["flashattntile_amd/csrc/kvwrite.hip", "flashattntile_amd/csrc/fat_common.h"],
 }
 

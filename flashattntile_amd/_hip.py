@@ -37,6 +37,7 @@ KERNEL_DECODE_GENERIC = 3
 KERNEL_PREFILL_PINGPONG = 1
 KERNEL_PREFILL_4WAVE = 2
 KERNEL_PREFILL_4WAVE_SPLIT = 3
+KERNEL_PREFILL_WIDE = 4
 
 # enum fat_rows (the `rows` field of the paged prefill arguments)
 ROWS_AUTO = 0

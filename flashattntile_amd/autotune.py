@@ -353,9 +353,11 @@ def build_config_space(kind: str, *, batch: int = 1, num_heads: int = 32, num_kv
     :func:`decode_partition` pick; the VALU kernel is left out for
     multi-token decode, which only the MFMA kernel serves.  ``prefill`` and
     ``prefill_paged``: the 8-wave ping-pong, the 4-wave kernel and its 8-wave
-    key-split form.
+    key-split form (and, packed only, the 64-rows-per-wave "wide" kernel).
     """
-    if kind in ("prefill", "prefill_paged"):
+    if kind == "prefill":
+        return [{"kernel": "pingpong"}, {"kernel": "wide"}, {"kernel": "4wave"}, {"kernel": "4wave_split"}]
+    if kind == "prefill_paged":
         return [{"kernel": "pingpong"}, {"kernel": "4wave"}, {"kernel": "4wave_split"}]
     if kind != "decode":
         raise ValueError(f"unknown kind {kind!r}")

@@ -53,36 +53,9 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "fat_common.h"
+#include "prefill_common.h"
 
 namespace fat {
-
-struct PrefillParams {
-  const uint8_t* q;
-  const uint8_t* k;
-  const uint8_t* v;
-  const int32_t* cu_q;
-  const int32_t* cu_k;
-  uint8_t* out;
-  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // element strides (k/v_st: slot stride when paged)
-  int32_t B, H, Hkv, group, nqb;
-  float scale_log2;
-  // Paged K/V (PAGED instantiations only).
-  const int32_t* pt;    // page table [B, max_pages]
-  const int32_t* lens;  // kv_len per sequence
-  int64_t pt_sb;        // page-table row stride
-  int64_t k_sp, v_sp;   // page strides (elements)
-  int32_t pshift;       // log2(page_size)
-  int32_t num_pages, max_pages;
-  // bf16 V converted ahead of the kernel (VPRE instantiations): v points at
-  // fp16 values scaled by 2^-v_head_scale[sequence * Hkv + kv head].
-  const int32_t* v_head_scale;
-};
-
-constexpr int kBM = 128;
-constexpr int kBN = 64;
-// Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
-constexpr int kBufFlags = 0x00020000;
 
 // Rows of a K or V stream read through the page table.  A lane loads LOADS
 // 16-byte chunks per tile, at rows row0 + u * RPL (u < LOADS) of the tile and
@@ -272,6 +245,12 @@ constexpr float kLazy = 8.0f;
 #ifndef FAT_PF_PP_MIN_CAUSAL
 #define FAT_PF_PP_MIN_CAUSAL 256
 #endif
+#ifndef FAT_PF_WIDE_MIN_FULL
+#define FAT_PF_WIDE_MIN_FULL 256
+#endif
+#ifndef FAT_PF_WIDE_MIN_CAUSAL
+#define FAT_PF_WIDE_MIN_CAUSAL 256
+#endif
 #ifndef FAT_PF_SPLIT_MAX
 #define FAT_PF_SPLIT_MAX 256
 #endif
@@ -281,53 +260,6 @@ constexpr float kLazy = 8.0f;
 #ifndef FAT_PF_SPLIT_LONG
 #define FAT_PF_SPLIT_LONG 32
 #endif
-
-// Epilogue of a wave that owns 32 query rows (row0 ..): O = acc / l (times
-// 2^e_acc for bf16) to the output, through `ob`, an LDS area of
-// kOutStage<D> elements (32 rows of D + 8) that no other wave touches
-// meanwhile: the wave writes its O^T fragments there as T, then each lane
-// stores 16 contiguous bytes of a row (8-byte pieces when the output rows
-// are not 16-byte aligned).
-template <int D> constexpr int kOutStage = 32 * (D + 8);
-template <typename T, int D, int DB>
-__device__ __forceinline__ void write_rows_via_lds(uint16_t* ob, int li, int g, int lane, const f32x16 (&acc)[DB],
-                                                   float l_run, int e_acc, bool vh, const PrefillParams& p,
-                                                   int q_start, int q_len, int h, int row0) {
-  constexpr int OS = D + 8;  // row stride (elements)
-  const float l_tot = xor32<OpAdd>(l_run);
-  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (vh) inv *= as_f32((u32)(127 + e_acc) << 23);
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int d0 = 32 * db + 4 * g + 8 * rr;
-      u32x2 pk;
-      pk[0] = Pair<T>::pack(acc[db][4 * rr + 0] * inv, acc[db][4 * rr + 1] * inv);
-      pk[1] = Pair<T>::pack(acc[db][4 * rr + 2] * inv, acc[db][4 * rr + 3] * inv);
-      *reinterpret_cast<u32x2*>(&ob[li * OS + d0]) = pk;
-    }
-  wave_lds_fence();
-  constexpr int CPR_O = D / 8;     // 16-byte chunks per row
-  constexpr int RPI = 64 / CPR_O;  // rows per store instruction
-  const int oc = lane % CPR_O;
-  const int orow = lane / CPR_O;
-  const bool o16 = ((reinterpret_cast<uintptr_t>(p.out) | (uintptr_t)(2 * p.o_st) | (uintptr_t)(2 * p.o_sh)) & 15) == 0;
-#pragma unroll
-  for (int i = 0; i < 32 / RPI; ++i) {
-    const int r = i * RPI + orow;
-    const u32x4 val = *reinterpret_cast<const u32x4*>(&ob[r * OS + 8 * oc]);
-    if (row0 + r < q_len) {
-      uint8_t* dst = p.out + 2 * ((int64_t)(q_start + row0 + r) * p.o_st + (int64_t)h * p.o_sh + 8 * oc);
-      if (o16) {
-        *reinterpret_cast<u32x4*>(dst) = val;
-      } else {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{val[0], val[1]};
-        *reinterpret_cast<u32x2*>(dst + 8) = u32x2{val[2], val[3]};
-      }
-    }
-  }
-}
 
 // POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
 // is folded into the exponent's fma; otherwise scores are scaled first.
@@ -784,10 +716,6 @@ struct MfmaPhaseOrder {
     }
   }
 };
-// Lazy-rescale bound of the ping-pong kernel (log2 units) and the partial
-// row-sum level above which its exact softmax path runs.
-constexpr float kLazyPP = 15.0f;
-constexpr float kLazyPPSum = 32768.0f;  // 2^kLazyPP
 
 template <typename T, int D, bool CAUSAL, bool POS, int PG, bool VPRE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -1277,7 +1205,7 @@ void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hip
 constexpr int64_t kVpreMinMeanQ = 2048;
 
 // Kernel families of the prefill launch.
-enum PrefillKind { PF_PINGPONG, PF_4WAVE, PF_4WAVE_SPLIT };
+enum PrefillKind { PF_PINGPONG, PF_4WAVE, PF_4WAVE_SPLIT, PF_WIDE };
 
 // Bytes of the fp16 copy of V in the prefill workspace (256-byte aligned).
 size_t vpre_bytes_v16(int64_t total_k, int64_t hkv, int64_t d) {
@@ -1329,7 +1257,17 @@ int launch_prefill_d(const fat::PrefillParams& prm, int D, bool causal, PrefillK
 
 bool valid_prefill_kernel(int kernel) {
   return kernel == FAT_KERNEL_AUTO || kernel == FAT_KERNEL_PREFILL_PINGPONG || kernel == FAT_KERNEL_PREFILL_4WAVE ||
-         kernel == FAT_KERNEL_PREFILL_4WAVE_SPLIT;
+         kernel == FAT_KERNEL_PREFILL_4WAVE_SPLIT || kernel == FAT_KERNEL_PREFILL_WIDE;
+}
+
+// Whether the bf16 V pre-pass can run for a packed launch (its arrays fit
+// fat_prefill_workspace_bytes, and the dense fp16 copy keeps the kernels'
+// 32-bit per-sequence offsets); whether it pays is decided by the caller.
+bool vpre_fits(int64_t B, int64_t Hkv, int D, int64_t total_k, int64_t max_seqlen_k) {
+  if (D == 256 || total_k <= 0) return false;
+  if (max_seqlen_k * 2 * Hkv * D >= 0x7fffffffLL || 2 * Hkv * D >= (1 << 24)) return false;
+  const int64_t nblk = (total_k + fat::kVpreRows - 1) / fat::kVpreRows;
+  return 2 * B <= nblk + 1;
 }
 
 // Kernel choice and grid shared by fat_prefill_varlen and fat_prefill_paged.
@@ -1348,19 +1286,27 @@ bool valid_prefill_kernel(int kernel) {
 // the balance gained).  A non-AUTO `kernel` argument forces one kernel (the
 // tests run every kernel on every shape that way).
 PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t max_seqlen_k, bool causal,
-                                int kernel, int D) {
+                                int kernel, int D, int dtype, bool packed, bool vpre_ok) {
   const int64_t heads = B * H;
   const int64_t n_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM * heads;
   const int64_t n_4w = (max_seqlen_q + fat::kBM - 1) / fat::kBM * heads;
+  const int64_t n_wide = (max_seqlen_q + fat::kWideBM - 1) / fat::kWideBM * heads;
   const int64_t chain = (max_seqlen_k + fat::kBN - 1) / fat::kBN;
   PrefillKind kind = PF_4WAVE;
   if (causal ? n_pp > FAT_PF_PP_MIN_CAUSAL : n_pp >= FAT_PF_PP_MIN_FULL) kind = PF_PINGPONG;
   else if ((n_4w <= FAT_PF_SPLIT_MAX && chain >= FAT_PF_SPLIT_TILES) ||
            (causal && n_4w <= 2 * FAT_PF_SPLIT_MAX && chain >= FAT_PF_SPLIT_LONG))
     kind = PF_4WAVE_SPLIT;
+  // The 64-rows-per-wave kernel once its 512-row blocks alone cover the CUs
+  // (causal grids: more than that, as for the ping-pong kernel), for packed
+  // fp16 at head_dim 128, and bf16 whose V the pre-pass converts.
+  if (kind == PF_PINGPONG && packed && D == 128 && (dtype == FAT_DTYPE_F16 || vpre_ok) &&
+      (causal ? n_wide > FAT_PF_WIDE_MIN_CAUSAL : n_wide >= FAT_PF_WIDE_MIN_FULL))
+    kind = PF_WIDE;
   if (kernel != FAT_KERNEL_AUTO) {
     kind = kernel == FAT_KERNEL_PREFILL_PINGPONG ? PF_PINGPONG
            : kernel == FAT_KERNEL_PREFILL_4WAVE  ? PF_4WAVE
+           : kernel == FAT_KERNEL_PREFILL_WIDE   ? PF_WIDE
                                                  : PF_4WAVE_SPLIT;
   }
   if (D == 256) kind = PF_4WAVE;  // see launch_prefill
@@ -1368,24 +1314,20 @@ PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t 
 }
 
 // Workspace bytes of the bf16 V pre-pass of a packed launch, or 0 when the
-// launch converts V in the kernel instead.  The pre-pass runs on the
-// ping-pong kernel when the sequences average at least kVpreMinMeanQ query
-// tokens (where the copy costs less than it saves: the pre-pass reads V twice
-// and writes it once, while the kernel converts each V tile once per (query
-// block, query head) that stages it; measured (bf16, 32/8 heads, D128): 3-6 %
-// faster from a mean of 2048 query tokens per sequence, level at 1024, 1-5 %
-// slower at 512), when the dense fp16 copy keeps the kernel's 32-bit
-// per-sequence offsets, and when the sequences average at least 32 keys
-// (2 B <= nblk + 1), which keeps the per-sequence scale arrays inside
-// fat_prefill_workspace_bytes.  Layout: the fp16 copy [total_k, Hkv, D]
-// (256-byte aligned), tile maxima [Hkv, nblk + B], scales [B, Hkv].
+// launch converts V in the kernel instead.  The wide kernel needs the
+// pre-pass; the ping-pong kernel runs it when the sequences average at
+// least kVpreMinMeanQ query tokens (where the copy costs less than it saves:
+// the pre-pass reads V twice and writes it once, while the kernel converts
+// each V tile once per (query block, query head) that stages it; measured
+// (bf16, 32/8 heads, D128): 3-6 % faster from a mean of 2048 query tokens
+// per sequence, level at 1024, 1-5 % slower at 512).  vpre_fits bounds the
+// rest.  Layout: the fp16 copy [total_k, Hkv, D] (256-byte aligned), tile
+// maxima [Hkv, nblk + B], scales [B, Hkv].
 size_t vpre_need(PrefillKind kind, int dtype, int64_t B, int64_t Hkv, int D, int64_t total_q, int64_t total_k,
                  int64_t max_seqlen_k) {
-  if (dtype != FAT_DTYPE_BF16 || kind != PF_PINGPONG || D == 256 || total_k <= 0) return 0;
-  if (total_q < kVpreMinMeanQ * B) return 0;
-  if (max_seqlen_k * 2 * Hkv * D >= 0x7fffffffLL || 2 * Hkv * D >= (1 << 24)) return 0;
+  if (dtype != FAT_DTYPE_BF16 || !vpre_fits(B, Hkv, D, total_k, max_seqlen_k)) return 0;
+  if (kind != PF_WIDE && !(kind == PF_PINGPONG && total_q >= kVpreMinMeanQ * B)) return 0;
   const int64_t nblk = (total_k + fat::kVpreRows - 1) / fat::kVpreRows;
-  if (2 * B > nblk + 1) return 0;
   return vpre_bytes_v16(total_k, Hkv, D) + (size_t)(Hkv * (nblk + 2 * B)) * sizeof(int32_t);
 }
 
@@ -1393,7 +1335,14 @@ template <int PG>
 int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
                    float softmax_scale, int kernel, const char* who, hipStream_t stream, void* workspace = nullptr,
                    int total_k = 0, int total_q = 0) {
-  PrefillKind kind = choose_prefill_kind(prm.B, prm.H, max_seqlen_q, max_seqlen_k, causal, kernel, D);
+  const bool vpre_ok = PG == 0 && workspace && vpre_fits(prm.B, prm.Hkv, D, total_k, max_seqlen_k);
+  PrefillKind kind =
+      choose_prefill_kind(prm.B, prm.H, max_seqlen_q, max_seqlen_k, causal, kernel, D, dtype, PG == 0, vpre_ok);
+  if (kind == PF_WIDE && (PG != 0 || D != 128 || (dtype == FAT_DTYPE_BF16 && !vpre_ok))) {
+    fat_host::set_error("%s: the wide prefill kernel takes packed head_dim-128 launches (bf16 with the "
+                        "workspace of fat_prefill_varlen_workspace_bytes) only", who);
+    return FAT_E_UNSUPPORTED;
+  }
   // head_dim 256: O and Q alone take 192 registers per lane, so only the
   // 4-wave kernel (one wave per SIMD) runs it; its K/V tiles take 141 KB of
   // LDS, which leaves no room for the split's second group.
@@ -1404,7 +1353,7 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     }
     kind = PF_4WAVE;
   }
-  const int bm = kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
+  const int bm = kind == PF_WIDE ? fat::kWideBM : kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
   prm.nqb = (max_seqlen_q + bm - 1) / bm;
   prm.scale_log2 = softmax_scale * fat::kLog2e;
   const int64_t n = (int64_t)prm.nqb * prm.B * prm.H;
@@ -1453,6 +1402,7 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     prm.v_sh = D;
     prm.v_head_scale = seq_scale;
   }
+  if (kind == PF_WIDE) return fat_host::launch_prefill_wide(prm, dtype == FAT_DTYPE_BF16, causal, grid, stream);
   if (dtype == FAT_DTYPE_F16) return launch_prefill_d<fat::F16, PG>(prm, D, causal, kind, grid, stream);
   return launch_prefill_d<fat::BF16, PG>(prm, D, causal, kind, grid, stream);
 }
@@ -1469,8 +1419,9 @@ extern "C" size_t fat_prefill_varlen_workspace_bytes(const fat_prefill_args* a) 
   if (!a || a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->total_q <= 0 || a->total_k <= 0 ||
       a->max_seqlen_q <= 0 || a->max_seqlen_k < 0 || !valid_prefill_kernel(a->kernel))
     return 0;
+  const bool fits = vpre_fits(a->batch, a->num_kv_heads, a->head_dim, a->total_k, a->max_seqlen_k);
   const PrefillKind kind = choose_prefill_kind(a->batch, a->num_heads, a->max_seqlen_q, a->max_seqlen_k,
-                                               a->causal != 0, a->kernel, a->head_dim);
+                                               a->causal != 0, a->kernel, a->head_dim, a->dtype, true, fits);
   return vpre_need(kind, a->dtype, a->batch, a->num_kv_heads, a->head_dim, a->total_q, a->total_k,
                    a->max_seqlen_k);
 }
@@ -1500,7 +1451,7 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   }
   if (!valid_prefill_kernel(a->kernel)) {
     fat_host::set_error("fat_prefill_varlen: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
-                        "_PREFILL_4WAVE (2) or _PREFILL_4WAVE_SPLIT (3), got %d", a->kernel);
+                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3) or _PREFILL_WIDE (4), got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;

@@ -6,9 +6,10 @@ and PV on CDNA4 MFMA (v_mfma_f32_32x32x16_{f16,bf16}) with fp32
 accumulation; the Triton tile knobs (BLOCK_M/BLOCK_N/num_warps/num_stages)
 are validated as in the reference but the gfx950 kernels use their own fixed
 tiling.  The one gfx950 knob is ``kernel``: ``"pingpong"`` (8 waves, 256 query
-rows per workgroup), ``"4wave"`` (128 rows), ``"4wave_split"`` (8 waves, 128
-rows, the two 4-wave groups taking alternate key tiles) or None (chosen from
-the grid size and the longest key chain).  With ``config=None`` the stored winner for the shape is used
+rows per workgroup), ``"wide"`` (8 waves of 64 query rows, 512 per workgroup;
+packed prefill at head_dim 128), ``"4wave"`` (128 rows), ``"4wave_split"`` (8
+waves, 128 rows, the two 4-wave groups taking alternate key tiles) or None
+(chosen from the grid size and the longest key chain).  With ``config=None`` the stored winner for the shape is used
 (:func:`flashattntile_amd.autotune.best_config`, the reference's lookup at
 ``prefill.py:167-191``).  There is no CPU fallback: non-ROCm tensors or a
 dtype other than fp16/bf16 raise.
@@ -33,7 +34,8 @@ __all__ = ["DEFAULT_CONFIG", "PAGED_CONFIG", "prefill_attention", "prefill_launc
 DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3, "kernel": None}
 
 _KERNEL_CODES = {None: _hip.KERNEL_AUTO, "pingpong": _hip.KERNEL_PREFILL_PINGPONG,
-                 "4wave": _hip.KERNEL_PREFILL_4WAVE, "4wave_split": _hip.KERNEL_PREFILL_4WAVE_SPLIT}
+                 "4wave": _hip.KERNEL_PREFILL_4WAVE, "4wave_split": _hip.KERNEL_PREFILL_4WAVE_SPLIT,
+                 "wide": _hip.KERNEL_PREFILL_WIDE}
 
 # Paged prefill's one extra knob: how K/V rows are addressed (None = the
 # fastest form the page size allows; "wide" = wave-uniform page ids with
@@ -59,7 +61,8 @@ def _resolve_config(config: dict | None, kind: str | None = None, signature: str
     if resolved.get("rows") not in _ROWS_CODES:
         raise ValueError(f"rows must be None, 'wide' or 'lane', got {resolved['rows']!r}")
     if resolved["kernel"] not in _KERNEL_CODES:
-        raise ValueError(f"kernel must be None, 'pingpong', '4wave' or '4wave_split', got {resolved['kernel']!r}")
+        raise ValueError(f"kernel must be None, 'pingpong', 'wide', '4wave' or '4wave_split', "
+                         f"got {resolved['kernel']!r}")
     for key in ("BLOCK_M", "BLOCK_N"):
         val = resolved[key]
         if val <= 0 or val & (val - 1):
@@ -147,7 +150,7 @@ def prefill_launch(
 
     ``q``/``k``/``v`` must have a contiguous head_dim axis; ``max_seqlen_*``
     must bound every sequence (they size the launch grid).  ``kernel``:
-    None (library's choice), ``"pingpong"``, ``"4wave"`` or ``"4wave_split"``.
+    None (library's choice), ``"pingpong"``, ``"wide"``, ``"4wave"`` or ``"4wave_split"``.
     """
     if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("q, k, v need a contiguous head_dim axis")

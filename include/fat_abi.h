@@ -44,7 +44,8 @@ extern "C" {
 #endif
 
 /* 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
- *     the bf16 V pre-pass scales V per (sequence, KV head).
+ *     the bf16 V pre-pass scales V per (sequence, KV head);
+ *     FAT_KERNEL_PREFILL_WIDE.
  * 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
  *     uses the workspace for an fp16 copy of V (optional).
  * 9: fat_paged_decode_noalloc (allocation-free decode).
@@ -74,9 +75,13 @@ enum fat_kernel {
                                       page size and head_dim the ABI takes   */
   FAT_KERNEL_PREFILL_PINGPONG = 1, /* 8 waves, 256 query rows per workgroup   */
   FAT_KERNEL_PREFILL_4WAVE = 2,    /* 4 waves, 128 query rows per workgroup   */
-  FAT_KERNEL_PREFILL_4WAVE_SPLIT = 3 /* 8 waves, 128 query rows: two 4-wave
-                                        groups take alternate key tiles and
-                                        merge (m, l, O) at the end          */
+  FAT_KERNEL_PREFILL_4WAVE_SPLIT = 3, /* 8 waves, 128 query rows: two 4-wave
+                                         groups take alternate key tiles and
+                                         merge (m, l, O) at the end         */
+  FAT_KERNEL_PREFILL_WIDE = 4 /* 8 waves x 64 query rows (512 per workgroup):
+                                 packed fat_prefill_varlen at head_dim 128;
+                                 bf16 needs the workspace (an fp16 copy of
+                                 V), other shapes return FAT_E_UNSUPPORTED */
 };
 
 /* Row addressing of fat_prefill_paged (the `rows` field): AUTO picks the

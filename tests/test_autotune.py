@@ -145,7 +145,7 @@ def test_committed_store_is_well_formed():
             assert cfg.get("kernel") in (None, "valu", "mfma")
         else:
             assert kind in ("prefill", "prefill_paged") and set(cfg) == {"kernel"}
-            assert cfg["kernel"] in (None, "pingpong", "4wave", "4wave_split")
+            assert cfg["kernel"] in (None, "pingpong", "wide", "4wave", "4wave_split")
 
 
 def test_config_space():
@@ -158,8 +158,10 @@ def test_config_space():
     assert max(c["split_k"] for c in short) == 3  # at least one page per partition
     multi = at.build_config_space("decode", batch=32, max_pages=256, q_len=4)
     assert {c["kernel"] for c in multi} == {"mfma"}  # only the MFMA kernel takes several tokens
-    assert at.build_config_space("prefill") == [{"kernel": "pingpong"}, {"kernel": "4wave"},
+    assert at.build_config_space("prefill") == [{"kernel": "pingpong"}, {"kernel": "wide"}, {"kernel": "4wave"},
                                                 {"kernel": "4wave_split"}]
+    assert at.build_config_space("prefill_paged") == [{"kernel": "pingpong"}, {"kernel": "4wave"},
+                                                      {"kernel": "4wave_split"}]
     with pytest.raises(ValueError):
         at.build_config_space("train")
 

@@ -22,11 +22,12 @@ DEV = "cuda"
 ODD_LENS = [1, 17, 255, 1000]
 
 
-@pytest.fixture(params=["auto", "pingpong", "4wave", "4wave_split"])
+@pytest.fixture(params=["auto", "pingpong", "wide", "4wave", "4wave_split"])
 def kernel(request, monkeypatch):
     """Run the test with the library's automatic choice and with each prefill
-    kernel forced (8-wave ping-pong, 4-wave, 4-wave key split), whatever the
-    shape."""
+    kernel forced (8-wave ping-pong with 32 or 64 rows per wave, 4-wave,
+    4-wave key split), whatever the shape.  The wide kernel takes head_dim
+    128 only; tests with other head dims check that it refuses them."""
     if request.param != "auto":
         force_prefill_knobs(monkeypatch, kernel=request.param)
     return request.param
@@ -45,6 +46,10 @@ def test_prefill_matches_oracle(dtype, d, h, hk, causal, kernel):
     label = f"prefill {kernel} {dtype} D{d} H{h}/{hk} causal={causal}"
     print(label, flush=True)
     q, k, v, cu = make_varlen(ODD_LENS, h, hk, d, dtype, seed=d + h + hk, device=DEV)
+    if kernel == "wide" and d != 128:
+        with pytest.raises(RuntimeError, match="wide prefill kernel takes packed head_dim-128"):
+            prefill_attention(q, k, v, cu, cu, max(ODD_LENS), max(ODD_LENS), causal=causal)
+        return
     out = prefill_attention(q, k, v, cu, cu, max(ODD_LENS), max(ODD_LENS), causal=causal)
     torch.cuda.synchronize()
     assert out.shape == q.shape and out.dtype == dtype
@@ -247,6 +252,10 @@ def test_prefill_output_rows_only_8_byte_aligned(dtype, d, kernel):
     big = torch.zeros(q.shape[0], 8, d + 4, dtype=dtype, device=DEV)
     out = big[:, :, 4:]
     assert out.data_ptr() % 16 == 8 and (out.stride(1) * out.element_size()) % 16 == 8
+    if kernel == "wide" and d != 128:
+        with pytest.raises(RuntimeError, match="wide prefill kernel"):
+            prefill_launch(q, k, v, cu, cu, 300, 300, True, d ** -0.5, out=out, kernel=kernel)
+        return
     prefill_launch(q, k, v, cu, cu, 300, 300, True, d ** -0.5, out=out, kernel=None if kernel == "auto" else kernel)
     torch.cuda.synchronize()
     assert torch.all(big[:, :, :4] == 0)

@@ -62,7 +62,7 @@ def test_multi_token_decode_kernel_choice():
         paged_decode_attention_multi(q, cache, config={"split_k": 2, "kernel": "valu"})
 
 
-@pytest.mark.parametrize("kern", ["pingpong", "4wave", "4wave_split"])
+@pytest.mark.parametrize("kern", ["pingpong", "wide", "4wave", "4wave_split"])
 def test_prefill_kernel_field_selects_the_kernel(kern):
     """A forced prefill kernel passes parity, packed and paged, and the
     library's own choice for this shape (ping-pong: 384 blocks of 256 rows)
@@ -80,6 +80,10 @@ def test_prefill_kernel_field_selects_the_kernel(kern):
     assert_parity(out_cfg, ref, label=label)
     kc, vc, pt, sl = make_paged(lens, 8, 128, 16, torch.float16, seed=12, device=DEV)
     cache = PagedKVCache(kc, vc, pt, sl, 16)
+    if kern == "wide":  # packed prefill only
+        with pytest.raises(RuntimeError, match="wide prefill kernel takes packed"):
+            paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
+        return
     p_cfg = paged_prefill_attention(q, cache, cu, max(lens), config={"kernel": kern})
     torch.cuda.synchronize()
     ref_p = ref_attention_paged_prefill(q.cpu(), kc.cpu(), vc.cpu(), pt.cpu(), sl.cpu(), cu.cpu(), causal=True,
@@ -104,7 +108,7 @@ def test_store_routes_config_none_launches(tmp_path, monkeypatch):
     lens = [1, 255, 1000]
     qp, k, v, cu = make_varlen(lens, 32, 8, 128, torch.bfloat16, seed=22, device=DEV)
     psig = at.prefill_signature(3, 32, 8, 128, 1000, 1000, True)
-    for kern in ("pingpong", "4wave", "4wave_split"):
+    for kern in ("pingpong", "wide", "4wave", "4wave_split"):
         at.save_best("prefill", psig, {"kernel": kern})
         got = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True)
         want = prefill_attention(qp, k, v, cu, cu, 1000, 1000, causal=True, config={"kernel": kern})
