@@ -78,6 +78,14 @@ struct WideOrder {
   }
 };
 
+// MFMA-phase operand lookahead: entries (two MFMAs each) whose LDS reads are
+// in flight ahead of their MFMAs.  2 measured fastest; 1, 3 and 4 ran 4 %
+// slower (with 3 or 4 the compiler's register assignment serialises the V
+// reads).
+#ifndef FAT_WIDE_LOOK
+#define FAT_WIDE_LOOK 2
+#endif
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -381,7 +389,7 @@ void prefill_wide_kernel(const PrefillParams p) {
       __builtin_amdgcn_s_setprio(2);
       pv(bprev);
       qk(bk);
-      WideOrder<0, 4 * DB / 2 + KS, 2 * DB, 2>::apply();
+      WideOrder<0, 4 * DB / 2 + KS, 2 * DB, FAT_WIDE_LOOK>::apply();
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
