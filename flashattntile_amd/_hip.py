@@ -38,6 +38,7 @@ KERNEL_PREFILL_PINGPONG = 1
 KERNEL_PREFILL_4WAVE = 2
 KERNEL_PREFILL_4WAVE_SPLIT = 3
 KERNEL_PREFILL_WIDE = 4
+KERNEL_PREFILL_GENERIC = 5
 
 # enum fat_rows (the `rows` field of the paged prefill arguments)
 ROWS_AUTO = 0

@@ -251,6 +251,12 @@ constexpr float kLazy = 8.0f;
 #ifndef FAT_PF_WIDE_MIN_CAUSAL
 #define FAT_PF_WIDE_MIN_CAUSAL 256
 #endif
+#ifndef FAT_PF_WIDE_MEAN
+#define FAT_PF_WIDE_MEAN 2048
+#endif
+#ifndef FAT_PF_WIDE_MEAN_F16_CAUSAL
+#define FAT_PF_WIDE_MEAN_F16_CAUSAL 4096
+#endif
 #ifndef FAT_PF_SPLIT_MAX
 #define FAT_PF_SPLIT_MAX 256
 #endif
@@ -1257,8 +1263,13 @@ int launch_prefill_d(const fat::PrefillParams& prm, int D, bool causal, PrefillK
 
 bool valid_prefill_kernel(int kernel) {
   return kernel == FAT_KERNEL_AUTO || kernel == FAT_KERNEL_PREFILL_PINGPONG || kernel == FAT_KERNEL_PREFILL_4WAVE ||
-         kernel == FAT_KERNEL_PREFILL_4WAVE_SPLIT || kernel == FAT_KERNEL_PREFILL_WIDE;
+         kernel == FAT_KERNEL_PREFILL_4WAVE_SPLIT || kernel == FAT_KERNEL_PREFILL_WIDE ||
+         kernel == FAT_KERNEL_PREFILL_GENERIC;
 }
+
+// fp32 and head_dim 16 / 512 have no MFMA prefill kernel: the generic one
+// (prefill_generic.hip) takes them; forcing it runs it on any shape.
+bool prefill_needs_generic(int dtype, int D) { return dtype == FAT_DTYPE_F32 || D == 16 || D == 512; }
 
 // Whether the bf16 V pre-pass can run for a packed launch (its arrays fit
 // fat_prefill_workspace_bytes, and the dense fp16 copy keeps the kernels'
@@ -1286,7 +1297,7 @@ bool vpre_fits(int64_t B, int64_t Hkv, int D, int64_t total_k, int64_t max_seqle
 // the balance gained).  A non-AUTO `kernel` argument forces one kernel (the
 // tests run every kernel on every shape that way).
 PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t max_seqlen_k, bool causal,
-                                int kernel, int D, int dtype, bool packed, bool vpre_ok) {
+                                int kernel, int D, int dtype, bool packed, bool vpre_ok, int64_t total_q) {
   const int64_t heads = B * H;
   const int64_t n_pp = (max_seqlen_q + fat::kPBM - 1) / fat::kPBM * heads;
   const int64_t n_4w = (max_seqlen_q + fat::kBM - 1) / fat::kBM * heads;
@@ -1299,9 +1310,15 @@ PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t 
     kind = PF_4WAVE_SPLIT;
   // The 64-rows-per-wave kernel once its 512-row blocks alone cover the CUs
   // (causal grids: more than that, as for the ping-pong kernel), for packed
-  // fp16 at head_dim 128, and bf16 whose V the pre-pass converts.
+  // fp16 at head_dim 128, and bf16 whose V the pre-pass converts, when the
+  // sequences are long on average: a sequence's last block is partly empty,
+  // and a 512-row block with one working wave takes as long as a full one.
+  // Measured (32/8 heads, D128, one box): fp16 causal gains 5 % at L8192,
+  // breaks even at 4 x 4096 and loses 3 % on the mixed pack of 8 (mean 2435
+  // queries); bf16 and non-causal gain from a mean of 2048.
+  const int64_t wide_mean = (dtype == FAT_DTYPE_F16 && causal) ? FAT_PF_WIDE_MEAN_F16_CAUSAL : FAT_PF_WIDE_MEAN;
   if (kind == PF_PINGPONG && packed && D == 128 && (dtype == FAT_DTYPE_F16 || vpre_ok) &&
-      (causal ? n_wide > FAT_PF_WIDE_MIN_CAUSAL : n_wide >= FAT_PF_WIDE_MIN_FULL))
+      (causal ? n_wide > FAT_PF_WIDE_MIN_CAUSAL : n_wide >= FAT_PF_WIDE_MIN_FULL) && total_q >= wide_mean * B)
     kind = PF_WIDE;
   if (kernel != FAT_KERNEL_AUTO) {
     kind = kernel == FAT_KERNEL_PREFILL_PINGPONG ? PF_PINGPONG
@@ -1335,9 +1352,24 @@ template <int PG>
 int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen_k, int dtype, int D, bool causal,
                    float softmax_scale, int kernel, const char* who, hipStream_t stream, void* workspace = nullptr,
                    int total_k = 0, int total_q = 0) {
+  if (prefill_needs_generic(dtype, D) || kernel == FAT_KERNEL_PREFILL_GENERIC) {
+    if (kernel != FAT_KERNEL_AUTO && kernel != FAT_KERNEL_PREFILL_GENERIC) {
+      fat_host::set_error("%s: %s runs on the generic prefill kernel only (kernel %d)", who,
+                          dtype == FAT_DTYPE_F32 ? "fp32" : "this head_dim", kernel);
+      return FAT_E_UNSUPPORTED;
+    }
+    prm.nqb = (max_seqlen_q + 31) / 32;
+    prm.scale_log2 = softmax_scale * fat::kLog2e;
+    const int64_t n = (int64_t)prm.nqb * prm.B * prm.H;
+    if (n > 0x7fffffff) {
+      fat_host::set_error("%s: too many query blocks (%lld)", who, (long long)n);
+      return FAT_E_UNSUPPORTED;
+    }
+    return fat_host::launch_prefill_generic(prm, dtype, D, causal, PG != 0, dim3((unsigned)n), stream);
+  }
   const bool vpre_ok = PG == 0 && workspace && vpre_fits(prm.B, prm.Hkv, D, total_k, max_seqlen_k);
-  PrefillKind kind =
-      choose_prefill_kind(prm.B, prm.H, max_seqlen_q, max_seqlen_k, causal, kernel, D, dtype, PG == 0, vpre_ok);
+  PrefillKind kind = choose_prefill_kind(prm.B, prm.H, max_seqlen_q, max_seqlen_k, causal, kernel, D, dtype,
+                                         PG == 0, vpre_ok, total_q);
   if (kind == PF_WIDE && (PG != 0 || D != 128 || (dtype == FAT_DTYPE_BF16 && !vpre_ok))) {
     fat_host::set_error("%s: the wide prefill kernel takes packed head_dim-128 launches (bf16 with the "
                         "workspace of fat_prefill_varlen_workspace_bytes) only", who);
@@ -1419,9 +1451,11 @@ extern "C" size_t fat_prefill_varlen_workspace_bytes(const fat_prefill_args* a) 
   if (!a || a->batch <= 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->total_q <= 0 || a->total_k <= 0 ||
       a->max_seqlen_q <= 0 || a->max_seqlen_k < 0 || !valid_prefill_kernel(a->kernel))
     return 0;
+  if (prefill_needs_generic(a->dtype, a->head_dim) || a->kernel == FAT_KERNEL_PREFILL_GENERIC) return 0;
   const bool fits = vpre_fits(a->batch, a->num_kv_heads, a->head_dim, a->total_k, a->max_seqlen_k);
   const PrefillKind kind = choose_prefill_kind(a->batch, a->num_heads, a->max_seqlen_q, a->max_seqlen_k,
-                                               a->causal != 0, a->kernel, a->head_dim, a->dtype, true, fits);
+                                               a->causal != 0, a->kernel, a->head_dim, a->dtype, true, fits,
+                                               a->total_q);
   return vpre_need(kind, a->dtype, a->batch, a->num_kv_heads, a->head_dim, a->total_q, a->total_k,
                    a->max_seqlen_k);
 }
@@ -1445,29 +1479,32 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
                         a->num_kv_heads);
     return FAT_E_INVALID;
   }
-  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16) {
-    fat_host::set_error("fat_prefill_varlen: dtype must be fp16 or bf16");
+  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16 && a->dtype != FAT_DTYPE_F32) {
+    fat_host::set_error("fat_prefill_varlen: dtype must be fp16, bf16 or fp32");
     return FAT_E_UNSUPPORTED;
   }
+  const int64_t esz = a->dtype == FAT_DTYPE_F32 ? 4 : 2;  // bytes per element
   if (!valid_prefill_kernel(a->kernel)) {
     fat_host::set_error("fat_prefill_varlen: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
-                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3) or _PREFILL_WIDE (4), got %d", a->kernel);
+                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3), _PREFILL_WIDE (4) or _PREFILL_GENERIC (5), "
+                        "got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 32 && D != 64 && D != 128 && D != 256) {
-    fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (32, 64, 128 or 256)", D);
+  if (D < 16 || D > 512 || (D & (D - 1)) != 0) {
+    fat_host::set_error("fat_prefill_varlen: head_dim %d unsupported (a power of two from 16 to 512)", D);
     return FAT_E_UNSUPPORTED;
   }
   if (a->max_seqlen_q < 0 || a->max_seqlen_k < 0) {
     fat_host::set_error("fat_prefill_varlen: max_seqlen must be non-negative");
     return FAT_E_INVALID;
   }
-  const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)(2 * a->q_stride_t) |
-                            (uintptr_t)(2 * a->q_stride_h) | (uintptr_t)(2 * a->k_stride_t) |
-                            (uintptr_t)(2 * a->k_stride_h) | (uintptr_t)(2 * a->v_stride_t) |
-                            (uintptr_t)(2 * a->v_stride_h);
-  const uintptr_t align8 = (uintptr_t)a->out | (uintptr_t)(2 * a->out_stride_t) | (uintptr_t)(2 * a->out_stride_h);
+  const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->v | (uintptr_t)(esz * a->q_stride_t) |
+                            (uintptr_t)(esz * a->q_stride_h) | (uintptr_t)(esz * a->k_stride_t) |
+                            (uintptr_t)(esz * a->k_stride_h) | (uintptr_t)(esz * a->v_stride_t) |
+                            (uintptr_t)(esz * a->v_stride_h);
+  const uintptr_t align8 =
+      (uintptr_t)a->out | (uintptr_t)(esz * a->out_stride_t) | (uintptr_t)(esz * a->out_stride_h);
   if ((align16 & 15) || (align8 & 7)) {
     fat_host::set_error("fat_prefill_varlen: q/k/v rows must be 16-byte aligned and out rows 8-byte aligned");
     return FAT_E_INVALID;
@@ -1475,7 +1512,7 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
   // Per-sequence K/V byte offsets are 32-bit (row * 2 * stride, 24-bit
   // multiply): every kv_len is bounded by max_seqlen_k.
   const int64_t kv_stride = a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t;
-  if (kv_stride <= 0 || 2 * kv_stride >= (1 << 24) || (int64_t)a->max_seqlen_k * 2 * kv_stride >= 0x7fffffffLL) {
+  if (kv_stride <= 0 || esz * kv_stride >= (1 << 24) || (int64_t)a->max_seqlen_k * esz * kv_stride >= 0x7fffffffLL) {
     fat_host::set_error("fat_prefill_varlen: max_seqlen_k %d x token stride %lld exceeds the kernel's 32-bit "
                         "per-sequence K/V offsets", a->max_seqlen_k, (long long)kv_stride);
     return FAT_E_UNSUPPORTED;
@@ -1530,18 +1567,19 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
                         a->num_kv_heads);
     return FAT_E_INVALID;
   }
-  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16) {
-    fat_host::set_error("fat_prefill_paged: dtype must be fp16 or bf16");
+  if (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16 && a->dtype != FAT_DTYPE_F32) {
+    fat_host::set_error("fat_prefill_paged: dtype must be fp16, bf16 or fp32");
     return FAT_E_UNSUPPORTED;
   }
+  const int64_t esz = a->dtype == FAT_DTYPE_F32 ? 4 : 2;  // bytes per element
   if (!valid_prefill_kernel(a->kernel)) {
     fat_host::set_error("fat_prefill_paged: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
-                        "_PREFILL_4WAVE (2) or _PREFILL_4WAVE_SPLIT (3), got %d", a->kernel);
+                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3) or _PREFILL_GENERIC (5), got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 32 && D != 64 && D != 128 && D != 256) {
-    fat_host::set_error("fat_prefill_paged: head_dim %d unsupported (32, 64, 128 or 256)", D);
+  if (D < 16 || D > 512 || (D & (D - 1)) != 0) {
+    fat_host::set_error("fat_prefill_paged: head_dim %d unsupported (a power of two from 16 to 512)", D);
     return FAT_E_UNSUPPORTED;
   }
   const int P = a->page_size;
@@ -1562,11 +1600,12 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     return FAT_E_INVALID;
   }
   const uintptr_t align16 = (uintptr_t)a->q | (uintptr_t)a->k_cache | (uintptr_t)a->v_cache |
-                            (uintptr_t)(2 * a->q_stride_t) | (uintptr_t)(2 * a->q_stride_h) |
-                            (uintptr_t)(2 * a->k_stride_page) | (uintptr_t)(2 * a->k_stride_slot) |
-                            (uintptr_t)(2 * a->k_stride_head) | (uintptr_t)(2 * a->v_stride_page) |
-                            (uintptr_t)(2 * a->v_stride_slot) | (uintptr_t)(2 * a->v_stride_head);
-  const uintptr_t align8 = (uintptr_t)a->out | (uintptr_t)(2 * a->out_stride_t) | (uintptr_t)(2 * a->out_stride_h);
+                            (uintptr_t)(esz * a->q_stride_t) | (uintptr_t)(esz * a->q_stride_h) |
+                            (uintptr_t)(esz * a->k_stride_page) | (uintptr_t)(esz * a->k_stride_slot) |
+                            (uintptr_t)(esz * a->k_stride_head) | (uintptr_t)(esz * a->v_stride_page) |
+                            (uintptr_t)(esz * a->v_stride_slot) | (uintptr_t)(esz * a->v_stride_head);
+  const uintptr_t align8 =
+      (uintptr_t)a->out | (uintptr_t)(esz * a->out_stride_t) | (uintptr_t)(esz * a->out_stride_h);
   if ((align16 & 15) || (align8 & 7)) {
     fat_host::set_error("fat_prefill_paged: q and cache rows must be 16-byte aligned and out rows 8-byte aligned");
     return FAT_E_INVALID;

@@ -97,4 +97,9 @@ namespace fat_host {
 // kernel (prm.v / v_head_scale), at head_dim 128.  `grid` counts blocks of
 // fat::kWideBM query rows.
 int launch_prefill_wide(const fat::PrefillParams& prm, bool bf16, bool causal, dim3 grid, hipStream_t stream);
+// The generic VALU prefill (prefill_generic.hip) for a fat_dtype and a
+// power-of-two head_dim 16..512, packed or paged; `grid` counts blocks of 32
+// query rows.
+int launch_prefill_generic(const fat::PrefillParams& prm, int dtype, int D, bool causal, bool paged, dim3 grid,
+                           hipStream_t stream);
 }  // namespace fat_host

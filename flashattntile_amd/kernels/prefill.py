@@ -8,11 +8,15 @@ are validated as in the reference but the gfx950 kernels use their own fixed
 tiling.  The one gfx950 knob is ``kernel``: ``"pingpong"`` (8 waves, 256 query
 rows per workgroup), ``"wide"`` (8 waves of 64 query rows, 512 per workgroup;
 packed prefill at head_dim 128), ``"4wave"`` (128 rows), ``"4wave_split"`` (8
-waves, 128 rows, the two 4-wave groups taking alternate key tiles) or None
-(chosen from the grid size and the longest key chain).  With ``config=None`` the stored winner for the shape is used
+waves, 128 rows, the two 4-wave groups taking alternate key tiles),
+``"generic"`` (an fp32 VALU kernel, 32 query rows per workgroup) or None
+(chosen from the grid size and the longest key chain).  With
+``config=None`` the stored winner for the shape is used
 (:func:`flashattntile_amd.autotune.best_config`, the reference's lookup at
-``prefill.py:167-191``).  There is no CPU fallback: non-ROCm tensors or a
-dtype other than fp16/bf16 raise.
+``prefill.py:167-191``).  There is no CPU fallback: non-ROCm tensors raise.
+fp32 inputs, and head_dim 16 or 512, always run on ``"generic"`` (the
+reference sends fp32 to its fp32 torch path, ``prefill.py:286-290``);
+forcing ``"generic"`` runs it on any shape.
 
 ``paged_prefill_attention`` is the paged (chunked) form the reference lacks:
 the queries of each sequence attend to that sequence's keys in a
@@ -35,7 +39,9 @@ DEFAULT_CONFIG = {"BLOCK_M": 64, "BLOCK_N": 64, "num_warps": 4, "num_stages": 3,
 
 _KERNEL_CODES = {None: _hip.KERNEL_AUTO, "pingpong": _hip.KERNEL_PREFILL_PINGPONG,
                  "4wave": _hip.KERNEL_PREFILL_4WAVE, "4wave_split": _hip.KERNEL_PREFILL_4WAVE_SPLIT,
-                 "wide": _hip.KERNEL_PREFILL_WIDE}
+                 "wide": _hip.KERNEL_PREFILL_WIDE, "generic": _hip.KERNEL_PREFILL_GENERIC}
+
+_PREFILL_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 # Paged prefill's one extra knob: how K/V rows are addressed (None = the
 # fastest form the page size allows; "wide" = wave-uniform page ids with
@@ -61,7 +67,7 @@ def _resolve_config(config: dict | None, kind: str | None = None, signature: str
     if resolved.get("rows") not in _ROWS_CODES:
         raise ValueError(f"rows must be None, 'wide' or 'lane', got {resolved['rows']!r}")
     if resolved["kernel"] not in _KERNEL_CODES:
-        raise ValueError(f"kernel must be None, 'pingpong', 'wide', '4wave' or '4wave_split', "
+        raise ValueError(f"kernel must be None, 'pingpong', 'wide', '4wave', '4wave_split' or 'generic', "
                          f"got {resolved['kernel']!r}")
     for key in ("BLOCK_M", "BLOCK_N"):
         val = resolved[key]
@@ -150,7 +156,7 @@ def prefill_launch(
 
     ``q``/``k``/``v`` must have a contiguous head_dim axis; ``max_seqlen_*``
     must bound every sequence (they size the launch grid).  ``kernel``:
-    None (library's choice), ``"pingpong"``, ``"wide"``, ``"4wave"`` or ``"4wave_split"``.
+    None (library's choice), ``"pingpong"``, ``"wide"``, ``"4wave"``, ``"4wave_split"`` or ``"generic"``.
     """
     if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("q, k, v need a contiguous head_dim axis")
@@ -210,8 +216,8 @@ def prefill_attention(
     if not all(t.is_cuda for t in (q, k, v, cu_seqlens_q, cu_seqlens_k)):
         raise RuntimeError("prefill_attention: inputs must be ROCm device tensors; this build runs the gfx950 "
                            "HIP kernel only (no CPU or reference fallback)")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    if q.dtype not in _PREFILL_DTYPES:
+        raise ValueError(f"prefill_attention: dtype {q.dtype} is not fp16/bf16/fp32 (the HIP kernels' types)")
     q = q if q.stride(-1) == 1 else q.contiguous()
     k = k if k.stride(-1) == 1 else k.contiguous()
     v = v if v.stride(-1) == 1 else v.contiguous()
@@ -328,8 +334,8 @@ def paged_prefill_attention(
     if not q.is_cuda:
         raise RuntimeError("paged_prefill_attention: inputs must be ROCm device tensors; this build runs the "
                            "gfx950 HIP kernel only (no CPU or reference fallback)")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"paged_prefill_attention: dtype {q.dtype} is not fp16/bf16 (the HIP kernel's types)")
+    if q.dtype not in _PREFILL_DTYPES:
+        raise ValueError(f"paged_prefill_attention: dtype {q.dtype} is not fp16/bf16/fp32 (the HIP kernels' types)")
     sig = prefill_paged_signature(cache.batch_size, q.shape[1], cache.num_kv_heads, cache.head_dim,
                                   cache.page_size, int(max_seqlen_q), causal)
     cfg = _resolve_config(config, "prefill_paged", sig, defaults=PAGED_CONFIG)

@@ -45,7 +45,8 @@ extern "C" {
 
 /* 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
  *     the bf16 V pre-pass scales V per (sequence, KV head);
- *     FAT_KERNEL_PREFILL_WIDE.
+ *     FAT_KERNEL_PREFILL_WIDE; fp32 prefill and head_dim 16..512
+ *     (FAT_KERNEL_PREFILL_GENERIC).
  * 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
  *     uses the workspace for an fp16 copy of V (optional).
  * 9: fat_paged_decode_noalloc (allocation-free decode).
@@ -78,10 +79,13 @@ enum fat_kernel {
   FAT_KERNEL_PREFILL_4WAVE_SPLIT = 3, /* 8 waves, 128 query rows: two 4-wave
                                          groups take alternate key tiles and
                                          merge (m, l, O) at the end         */
-  FAT_KERNEL_PREFILL_WIDE = 4 /* 8 waves x 64 query rows (512 per workgroup):
-                                 packed fat_prefill_varlen at head_dim 128;
-                                 bf16 needs the workspace (an fp16 copy of
-                                 V), other shapes return FAT_E_UNSUPPORTED */
+  FAT_KERNEL_PREFILL_WIDE = 4, /* 8 waves x 64 query rows (512 per workgroup):
+                                  packed fat_prefill_varlen at head_dim 128;
+                                  bf16 needs the workspace (an fp16 copy of
+                                  V), other shapes return FAT_E_UNSUPPORTED */
+  FAT_KERNEL_PREFILL_GENERIC = 5 /* fp32 VALU kernel for every dtype and
+                                    power-of-two head_dim 16..512; the only
+                                    kernel for fp32 and head_dim 16 / 512 */
 };
 
 /* Row addressing of fat_prefill_paged (the `rows` field): AUTO picks the
@@ -190,9 +194,12 @@ typedef struct fat_decode_args {
  *   cu_seqlens_q / cu_seqlens_k int32 [batch + 1], starting at 0,
  *   non-decreasing, kv_len >= q_len per sequence when causal.
  *   out [total_q, num_heads, head_dim]      dtype
- * head_dim is 32, 64, 128 or 256; 256 runs on the 4-wave kernel only
- * (FAT_KERNEL_AUTO or FAT_KERNEL_PREFILL_4WAVE; the others return
- * FAT_E_UNSUPPORTED).  The same holds for fat_prefill_paged.
+ * dtype is fp16, bf16 or fp32; head_dim a power of two from 16 to 512.
+ * fp32 and head_dim 16 / 512 run on the generic kernel only
+ * (FAT_KERNEL_AUTO or FAT_KERNEL_PREFILL_GENERIC); head_dim 256 at fp16 /
+ * bf16 on the 4-wave kernel (or the generic one); a kernel that does not
+ * take the shape returns FAT_E_UNSUPPORTED.  The same holds for
+ * fat_prefill_paged.
  * Causal masking is bottom-right aligned: query i of a sequence sees key j
  * iff j <= i + (kv_len - q_len)  (flashattn_tile/reference.py:19-22).
  * `workspace` is optional: NULL, or 256-byte aligned and holding
@@ -226,9 +233,9 @@ typedef struct fat_prefill_args {
   int32_t max_seqlen_q;
   int32_t max_seqlen_k;
   int32_t causal;
-  int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
+  int32_t dtype; /* FAT_DTYPE_F16, FAT_DTYPE_BF16 or FAT_DTYPE_F32 */
   float softmax_scale;
-  int32_t kernel; /* FAT_KERNEL_AUTO, _PREFILL_PINGPONG or _PREFILL_4WAVE */
+  int32_t kernel; /* FAT_KERNEL_AUTO or a FAT_KERNEL_PREFILL_* */
 } fat_prefill_args;
 
 /*
@@ -271,9 +278,9 @@ typedef struct fat_prefill_paged_args {
   int32_t max_pages;
   int32_t max_seqlen_q;
   int32_t causal;
-  int32_t dtype; /* FAT_DTYPE_F16 or FAT_DTYPE_BF16 */
+  int32_t dtype; /* FAT_DTYPE_F16, FAT_DTYPE_BF16 or FAT_DTYPE_F32 */
   float softmax_scale;
-  int32_t kernel; /* FAT_KERNEL_AUTO, _PREFILL_PINGPONG or _PREFILL_4WAVE */
+  int32_t kernel; /* FAT_KERNEL_AUTO or a FAT_KERNEL_PREFILL_* (not WIDE) */
   int32_t rows;   /* FAT_ROWS_AUTO, _WIDE or _LANE                        */
 } fat_prefill_paged_args;
 

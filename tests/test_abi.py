@@ -143,7 +143,7 @@ def test_prefill_argument_errors_are_reported():
     for f in ("q", "k", "v", "cu_seqlens_q", "cu_seqlens_k", "out"):
         setattr(a, f, 0x1000)
     a.batch, a.num_heads, a.num_kv_heads, a.head_dim, a.dtype = 1, 4, 2, 128, _hip.DT_F16
-    a.kernel = 5
+    a.kernel = 6
     assert lib.fat_prefill_varlen(ctypes.byref(a), None) == 1 and "kernel" in _err()
     p = _hip.PrefillPagedArgs()
     for f in ("q", "k_cache", "v_cache", "page_table", "seq_lens", "cu_seqlens_q", "out"):
