@@ -1011,8 +1011,8 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
-  if (D != 32 && D != 64 && D != 128 && D != 256) {
-    fat_host::set_error("fat_paged_decode: head_dim %d unsupported (32, 64, 128 or 256)", D);
+  if (D < 16 || D > 512 || (D & (D - 1)) != 0) {
+    fat_host::set_error("fat_paged_decode: head_dim %d unsupported (a power of two from 16 to 512)", D);
     return FAT_E_UNSUPPORTED;
   }
   if (a->page_size < 1) {

@@ -1,7 +1,7 @@
 // decode_generic.hip -- paged decode for the shapes the VALU and MFMA decode
 // kernels (decode.hip) do not take: fp32 queries and caches, page sizes that
 // are not a power of two or are below the rows one 16-byte load per lane
-// covers, and head_dim 32 or 256.
+// covers, and head_dim 16, 32, 256 or 512.
 //
 // Semantics are those of the other decode kernels and of the reference's
 // native decode (csrc/paged_decode.cu:80-235): one query per sequence, query
@@ -19,7 +19,8 @@
 //   * thread (head, row) takes the whole q.k dot product of one (query head,
 //     token) pair from LDS; a 32-lane shuffle gives each head's tile max and
 //     sum for the online softmax;
-//   * thread (head, dims) accumulates its output dims over the tile's 32 rows.
+//   * thread (head, dims) accumulates its output dims over the tile's 32 rows
+//     (at head_dim 16 the 8 heads x 16 dims leave half the threads idle).
 // Three barriers per tile.  It is an HBM-streaming kernel like the others,
 // but it spends more VALU and LDS work per byte; the fast kernels keep every
 // shape they support.
@@ -38,9 +39,9 @@ __global__ __launch_bounds__(256) void paged_decode_generic_kernel(const DecodeP
   constexpr int NCH = TR * CPR;                            // chunks per tile of K (or V)
   constexpr int CPT = (NCH + NT - 1) / NT;                 // chunks per thread
   constexpr int KRS = D + 1;                               // LDS K row stride (floats)
-  constexpr int OPT = HM * D / NT;                         // output values per thread
+  constexpr int OPT = (HM * D + NT - 1) / NT;              // output values per thread
   static_assert(CPR >= 1 && CPR * EPC == D, "unsupported head_dim / element size");
-  static_assert(OPT >= 1 && OPT * NT == HM * D, "unsupported head_dim");
+  static_assert(OPT * NT == HM * D || (OPT == 1 && HM * D < NT), "unsupported head_dim");
 
   __shared__ float sK[TR * KRS];
   __shared__ float sV[TR * D];
@@ -256,6 +257,9 @@ namespace {
 template <typename QT, int KV>
 int launch_generic_kv(const fat::DecodeParams& prm, int D, int hpw, dim3 grid, hipStream_t stream) {
   switch (D) {
+    case 16:
+      hipLaunchKernelGGL((fat::paged_decode_generic_kernel<QT, KV, 16>), grid, dim3(256), 0, stream, prm, hpw);
+      break;
     case 32:
       hipLaunchKernelGGL((fat::paged_decode_generic_kernel<QT, KV, 32>), grid, dim3(256), 0, stream, prm, hpw);
       break;
@@ -268,8 +272,11 @@ int launch_generic_kv(const fat::DecodeParams& prm, int D, int hpw, dim3 grid, h
     case 256:
       hipLaunchKernelGGL((fat::paged_decode_generic_kernel<QT, KV, 256>), grid, dim3(256), 0, stream, prm, hpw);
       break;
+    case 512:
+      hipLaunchKernelGGL((fat::paged_decode_generic_kernel<QT, KV, 512>), grid, dim3(256), 0, stream, prm, hpw);
+      break;
     default:
-      fat_host::set_error("fat_paged_decode: head_dim %d unsupported (32, 64, 128 or 256)", D);
+      fat_host::set_error("fat_paged_decode: head_dim %d unsupported (a power of two from 16 to 512)", D);
       return FAT_E_UNSUPPORTED;
   }
   return fat_host::launch_status("paged_decode_generic_kernel");

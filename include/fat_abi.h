@@ -46,7 +46,8 @@ extern "C" {
 /* 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
  *     the bf16 V pre-pass scales V per (sequence, KV head);
  *     FAT_KERNEL_PREFILL_WIDE; fp32 prefill and head_dim 16..512
- *     (FAT_KERNEL_PREFILL_GENERIC).
+ *     (FAT_KERNEL_PREFILL_GENERIC); decode head_dim 16 and 512 (generic
+ *     decode kernel).
  * 10: fat_prefill_workspace_bytes is non-zero: bf16 fat_prefill_varlen
  *     uses the workspace for an fp16 copy of V (optional).
  * 9: fat_paged_decode_noalloc (allocation-free decode).
@@ -117,7 +118,7 @@ enum fat_status {
  *   page_table int32 [batch, max_pages]  (row stride page_table_stride)
  *   seq_lens int32 [batch]; a sequence of length <= 0 yields zeros, and
  *            lengths beyond max_pages*page_size are clamped to it
- * head_dim is 32, 64, 128 or 256 and page_size any positive number (page
+ * head_dim is a power of two from 16 to 512 and page_size any positive number (page
  * ids are clamped to [0, num_pages)).  The VALU and MFMA kernels take
  * fp16/bf16 queries, head_dim 64 or 128 and power-of-two pages of at least
  * the rows one 16-byte load per lane covers: 4 (fp16/bf16, head_dim 128), 8

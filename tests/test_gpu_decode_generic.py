@@ -87,9 +87,12 @@ def test_small_and_odd_pages(dtype, P):
         assert_parity(out, _ref32(q, cache), label=f"{label} sk{split_k}")
 
 
-@pytest.mark.parametrize("d", [32, 256])
+@pytest.mark.parametrize("d", [16, 32, 256, 512])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_head_dims_32_and_256(dtype, d):
+def test_head_dims_16_to_512(dtype, d):
+    """Head dims the fast kernels do not take (16, 32, 256, 512) run on the
+    generic kernel; at 16, 8 heads x 16 dims leave half its output threads
+    idle, at 512 its K/V tiles fill 128 KB of LDS."""
     label = f"generic D{d} {dtype}"
     print(label, flush=True)
     q, cache = _case(LENS + [4096], 16, 4, d, 16, dtype, seed=d)
@@ -121,6 +124,24 @@ def test_quant_small_pages(mode, qdtype, P):
     cache = PagedKVCache(qk.to(DEV), qv.to(DEV), pt.to(DEV), sl.to(DEV), P)
     ref = ref_attention_paged(q.cpu(), quant_ref.dequantize_pages(qk, sk, qdtype),
                               quant_ref.dequantize_pages(qv, sv, qdtype), pt, sl, return_fp32=True)
+    for split_k in (1, 3):
+        out = paged_decode_attention_fp8(q, cache, {"k": sk.to(DEV), "v": sv.to(DEV)}, config={"split_k": split_k})
+        torch.cuda.synchronize()
+        assert_parity(out, ref, label=f"{label} sk{split_k}")
+
+
+@pytest.mark.parametrize("d", [16, 512])
+@pytest.mark.parametrize("mode", ["int8", "float8_e4m3fn"])
+def test_quant_head_dims_16_and_512(mode, d):
+    label = f"generic quant {mode} D{d}"
+    print(label, flush=True)
+    k, v, pt, sl = make_paged(LENS, 4, d, 16, torch.float32, seed=d + 3, device="cpu")
+    qk, sk = quant_ref.quantize_pages(k, mode)
+    qv, sv = quant_ref.quantize_pages(v, mode)
+    q = make_query(len(LENS), 16, d, torch.float16, seed=d + 4, device=DEV)
+    cache = PagedKVCache(qk.to(DEV), qv.to(DEV), pt.to(DEV), sl.to(DEV), 16)
+    ref = ref_attention_paged(q.cpu(), quant_ref.dequantize_pages(qk, sk, torch.float16),
+                              quant_ref.dequantize_pages(qv, sv, torch.float16), pt, sl, return_fp32=True)
     for split_k in (1, 3):
         out = paged_decode_attention_fp8(q, cache, {"k": sk.to(DEV), "v": sv.to(DEV)}, config={"split_k": split_k})
         torch.cuda.synchronize()
