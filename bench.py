@@ -37,10 +37,11 @@ import time
 
 import torch
 
-from flashattntile_amd.env import peak_hbm_gbs, peak_mfma_tflops  # noqa: E402
+from flashattntile_amd.env import MI355X, peak_hbm_gbs, peak_mfma_tflops  # noqa: E402
 
 HBM_PEAK_GBS = peak_hbm_gbs()
 MFMA_PEAK_TFLOPS = peak_mfma_tflops("fp16")  # dense fp16 / bf16
+VALU_FP32_PEAK_TFLOPS = MI355X["vector_fp32_tflops"]  # the generic fp32 prefill kernel's bound
 MALL_BYTES = 256 << 20
 FLUSH_BYTES = 512 << 20
 
@@ -370,7 +371,8 @@ def run_prefill(lens, dtype, device, steps, warmup, hq=32, hkv=8, d=128, seed=7,
     else:
         ms = _time_steps(step, steps, warmup, stream)
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flops": flops, "frac": tflops / MFMA_PEAK_TFLOPS, **extra}
+    peak = VALU_FP32_PEAK_TFLOPS if dtype == torch.float32 else MFMA_PEAK_TFLOPS
+    return {"ms": ms, "tflops": tflops, "flops": flops, "frac": tflops / peak, "peak": peak, **extra}
 
 
 PREFILL_SEQ = 8192
@@ -521,7 +523,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
-    kv_elem = 1 if quant else 2
+    kv_elem = 1 if quant else torch.tensor([], dtype=dtype).element_size()
     pool_bytes = sum(lens) * hkv * d * 2 * kv_elem
     copies = 1 if pool_bytes >= 2 * MALL_BYTES else 2
     q, pools, table, seq, table_cpu, seq_cpu = _paged_inputs(lens, hq, hkv, d, page, dtype, seed=11,
@@ -645,7 +647,7 @@ def _prefill_row(name, lens, dtype, device, args, hq=32, hkv=8, d=128):
     cpu_flops = flops_attention_varlen(group, d, [L], [L], causal=True)
     torch.cuda.empty_cache()
     return {"config": name, "kind": "prefill", "value": round(r["tflops"], 1), "unit": "TFLOP/s",
-            "frac": round(r["frac"], 4), "us": round(r["ms"] * 1e3, 2), "flops": r["flops"],
+            "frac": round(r["frac"], 4), "peak": r["peak"], "us": round(r["ms"] * 1e3, 2), "flops": r["flops"],
             "cpu": {"value": round(cpu_flops / best / 1e12, 5), "unit": "TFLOP/s",
                     "sample": f"{group} query heads / 1 KV head of sequence 0 (L={L}), min of {reps}"}}
 
@@ -677,9 +679,19 @@ def _paged_prefill_row(name, lens_k, lens_q, dtype, device, args, page=16, hq=32
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
     mq = max(lens_q)
+    # The product's launch (kernels/prefill.py paged_prefill_launch): the
+    # workspace the library asks for (packed K/V copies for long chunks),
+    # allocated once outside the timed steps.
+    a = _hip.prefill_paged_args(q, k, v, table, seq, cu, out, page, mq, True, d ** -0.5)
+    need = _hip.prefill_paged_workspace_bytes(a)
+    ws = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+    if ws is not None:
+        a.workspace = ws.data_ptr()
+    launch, ref, hs = _hip.lib().fat_prefill_paged, ctypes.byref(a), ctypes.c_void_p(handle)
 
     def step(i):
-        _hip.prefill_paged(q, k, v, table, seq, cu, out, page, mq, True, d ** -0.5, stream=handle)
+        if launch(ref, hs) != 0:
+            raise RuntimeError(_hip.lib().fat_last_error().decode(errors="replace"))
 
     ms = _time_steps(step, max(10, args.steps // 10), 3, stream)
     flops = flops_attention_varlen(hq, d, lens_q, lens_k, causal=True)
@@ -697,6 +709,7 @@ def _paged_prefill_row(name, lens_k, lens_q, dtype, device, args, page=16, hq=32
     torch.cuda.empty_cache()
     return {"config": name, "kind": "prefill_paged", "value": round(tflops, 1), "unit": "TFLOP/s",
             "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "us": round(ms * 1e3, 2), "flops": flops,
+            "workspace_bytes": need,
             "cpu": {"value": round(cpu_flops / best / 1e12, 5), "unit": "TFLOP/s",
                     "sample": f"{group} query heads / 1 KV head of sequence 0, min of {reps}"}}
 
@@ -940,6 +953,9 @@ def all_configs(args, device):
         for L in (512, 1024, 2048, 4096, 8192):
             emit(_prefill_row(f"prefill {dn} causal L{L}", [L], dt, device, args))
         emit(_prefill_row(f"prefill {dn} causal mixed8 {sum(mixed)} tok", mixed, dt, device, args))
+    # fp32 prefill: the generic VALU kernel (its bound is the 157.3 TFLOP/s fp32 vector peak)
+    for L in (1024, 4096):
+        emit(_prefill_row(f"prefill fp32 causal L{L} (generic)", [L], torch.float32, device, args))
     # quantised decode B128 ctx16384
     for mode, mn in (("int8", "int8"), ("float8_e4m3fn", "fp8")):
         emit(_decode_row(f"decode {mn} B128 ctx16384", [16384] * 128, 32, 8, 128, 16, device, args, flush,
@@ -956,6 +972,13 @@ def all_configs(args, device):
     emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
     for page in (32, 64):
         emit(_decode_row(f"decode fp16 P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device, args, flush))
+    # the generic decode kernel (LDS-tiled, any page size): fp32, and pages of 1 and 5 rows
+    for dt, dn in ((torch.float32, "fp32"), (torch.float16, "fp16")):
+        for page in (1, 5):
+            emit(_decode_row(f"decode {dn} generic P{page} B32 ctx4096", [4096] * 32, 32, 8, 128, page, device,
+                             args, flush, dtype=dt))
+    emit(_decode_row("decode fp32 generic P16 B32 ctx4096", [4096] * 32, 32, 8, 128, 16, device, args, flush,
+                     dtype=torch.float32))
     # Multi-token (speculative) decode: T query tokens per sequence
     for T in (2, 4, 8):
         emit(_multi_decode_row(f"decode fp16 multi-token T{T} B32 ctx4096", [4096] * 32, T, device, args))

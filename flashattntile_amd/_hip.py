@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # enum fat_dtype
 DT_F16 = 0
@@ -54,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "fat_prefill_workspace_bytes",
     "fat_prefill_varlen_workspace_bytes",
     "fat_prefill_varlen",
+    "fat_prefill_paged_workspace_bytes",
     "fat_prefill_paged",
     "fat_quantize_pages",
     "fat_append_kv",
@@ -180,6 +181,7 @@ class PrefillPagedArgs(ctypes.Structure):
         ("softmax_scale", ctypes.c_float),
         ("kernel", _c_i32),
         ("rows", _c_i32),
+        ("workspace", _c_vp),
     ]
 
 
@@ -293,6 +295,8 @@ def _load() -> None:
         lib.fat_prefill_varlen_workspace_bytes.argtypes = [ctypes.POINTER(PrefillArgs)]
         lib.fat_prefill_varlen.restype = ctypes.c_int
         lib.fat_prefill_varlen.argtypes = [ctypes.POINTER(PrefillArgs), _c_vp]
+        lib.fat_prefill_paged_workspace_bytes.restype = ctypes.c_size_t
+        lib.fat_prefill_paged_workspace_bytes.argtypes = [ctypes.POINTER(PrefillPagedArgs)]
         lib.fat_prefill_paged.restype = ctypes.c_int
         lib.fat_prefill_paged.argtypes = [ctypes.POINTER(PrefillPagedArgs), _c_vp]
         lib.fat_quantize_pages.restype = ctypes.c_int
@@ -535,6 +539,15 @@ def prefill_args(
     return a
 
 
+def prefill_paged_workspace_bytes(a: PrefillPagedArgs) -> int:
+    """Workspace bytes the paged launch of ``a`` uses (0: it runs without one)."""
+    return int(lib().fat_prefill_paged_workspace_bytes(ctypes.byref(a)))
+
+
+def prefill_paged_with_args(a: PrefillPagedArgs, stream: int) -> None:
+    _check(lib().fat_prefill_paged(ctypes.byref(a), _c_vp(stream)), "fat_prefill_paged")
+
+
 def prefill_paged(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -550,8 +563,34 @@ def prefill_paged(
     stream: int | None = None,
     kernel: int = KERNEL_AUTO,
     rows: int = ROWS_AUTO,
+    workspace: torch.Tensor | None = None,
 ) -> None:
-    """Enqueue ``fat_prefill_paged`` for already-validated device tensors."""
+    """Enqueue ``fat_prefill_paged`` for already-validated device tensors
+    (``workspace``: None, or at least :func:`prefill_paged_workspace_bytes`
+    of the launch, 256-byte aligned)."""
+    a = prefill_paged_args(q, k_cache, v_cache, page_table, seq_lens, cu_seqlens_q, out, page_size, max_seqlen_q,
+                           causal, softmax_scale, kernel, rows, workspace)
+    handle = current_stream_handle(q.device) if stream is None else stream
+    prefill_paged_with_args(a, handle)
+
+
+def prefill_paged_args(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    page_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    out: torch.Tensor,
+    page_size: int,
+    max_seqlen_q: int,
+    causal: bool,
+    softmax_scale: float,
+    kernel: int = KERNEL_AUTO,
+    rows: int = ROWS_AUTO,
+    workspace: torch.Tensor | None = None,
+) -> PrefillPagedArgs:
+    """The ``fat_prefill_paged_args`` block of a launch."""
     a = PrefillPagedArgs()
     a.q = _ptr(q)
     a.k_cache = _ptr(k_cache)
@@ -579,8 +618,8 @@ def prefill_paged(
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
     a.rows = int(rows)
-    handle = current_stream_handle(q.device) if stream is None else stream
-    _check(lib().fat_prefill_paged(ctypes.byref(a), _c_vp(handle)), "fat_prefill_paged")
+    a.workspace = _ptr(workspace)
+    return a
 
 
 def quantize_pages(src: torch.Tensor, dst: torch.Tensor, scale: torch.Tensor, stream: int | None = None) -> None:

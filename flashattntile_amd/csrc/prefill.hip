@@ -1547,6 +1547,55 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
                            a->total_k, a->total_q);
 }
 
+// Staging plan of a paged launch (prefill_stage.hip): the rows of packed K/V
+// copies (batch x max_pages x page_size, the table's capacity) when the
+// launch runs on the wide kernel through them, else 0.  Taken when the packed
+// launch of the same shape would run the wide kernel (fp16, or bf16 whose
+// copied V the pre-pass converts; head_dim 128; sequences averaging
+// FAT_PF_WIDE_MEAN queries or more, choose_prefill_kind), when the copies
+// hold at most 4 rows per query (the workspace stays in proportion to the
+// launch) and fit the packed kernels' 32-bit offsets.  The copies cost one
+// read and one write of the used K/V rows; the wide kernel then reads each
+// row once per query block, 16 bytes a lane straight into LDS.
+int64_t paged_stage_rows(const fat_prefill_paged_args* a) {
+  if (a->head_dim != 128 || (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16)) return 0;
+  if (a->kernel != FAT_KERNEL_AUTO && a->kernel != FAT_KERNEL_PREFILL_WIDE) return 0;
+  if (a->batch <= 0 || a->batch > 65535 || a->total_q <= 0 || a->max_seqlen_q <= 0 || a->num_kv_heads <= 0 ||
+      a->num_heads <= 0 || a->max_pages <= 0 || a->page_size <= 0)
+    return 0;
+  const int64_t cap = (int64_t)a->max_pages * a->page_size;
+  const int64_t rows = cap * a->batch;
+  if (rows > 4 * (int64_t)a->total_q || rows * a->num_kv_heads * a->head_dim * 2 >= 0x7fffffffLL) return 0;
+  const bool fits = vpre_fits(a->batch, a->num_kv_heads, a->head_dim, rows, cap);
+  if (a->dtype == FAT_DTYPE_BF16 && !fits) return 0;
+  const PrefillKind kind = choose_prefill_kind(a->batch, a->num_heads, a->max_seqlen_q, cap, a->causal != 0,
+                                               a->kernel, a->head_dim, a->dtype, true, fits, a->total_q);
+  return kind == PF_WIDE ? rows : 0;
+}
+
+// Workspace of a staged paged launch (256-byte aligned parts): cu_k [B + 1],
+// the K and V copies [rows, Hkv, D], then the bf16 V pre-pass area.
+struct PagedStageLayout {
+  size_t k, v, vpre, total;
+};
+PagedStageLayout paged_stage_layout(const fat_prefill_paged_args* a, int64_t rows) {
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t kv = al((size_t)rows * a->num_kv_heads * a->head_dim * 2);
+  PagedStageLayout L;
+  L.k = al((size_t)(a->batch + 1) * sizeof(int32_t));
+  L.v = L.k + kv;
+  L.vpre = L.v + kv;
+  L.total = L.vpre + vpre_need(PF_WIDE, a->dtype, a->batch, a->num_kv_heads, a->head_dim, a->total_q, rows,
+                               (int64_t)a->max_pages * a->page_size);
+  return L;
+}
+
+extern "C" size_t fat_prefill_paged_workspace_bytes(const fat_prefill_paged_args* a) {
+  if (!a) return 0;
+  const int64_t rows = paged_stage_rows(a);
+  return rows > 0 ? paged_stage_layout(a, rows).total : 0;
+}
+
 extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_ptr) {
   fat_host::clear_error();
   if (!a) {
@@ -1574,7 +1623,8 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   const int64_t esz = a->dtype == FAT_DTYPE_F32 ? 4 : 2;  // bytes per element
   if (!valid_prefill_kernel(a->kernel)) {
     fat_host::set_error("fat_prefill_paged: kernel must be FAT_KERNEL_AUTO (0), _PREFILL_PINGPONG (1), "
-                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3) or _PREFILL_GENERIC (5), got %d", a->kernel);
+                        "_PREFILL_4WAVE (2), _PREFILL_4WAVE_SPLIT (3), _PREFILL_WIDE (4) or _PREFILL_GENERIC (5), "
+                        "got %d", a->kernel);
     return FAT_E_INVALID;
   }
   const int D = a->head_dim;
@@ -1610,6 +1660,17 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
     fat_host::set_error("fat_prefill_paged: q and cache rows must be 16-byte aligned and out rows 8-byte aligned");
     return FAT_E_INVALID;
   }
+  const int64_t stage_rows = paged_stage_rows(a);
+  if (a->kernel == FAT_KERNEL_PREFILL_WIDE && (stage_rows == 0 || !a->workspace)) {
+    fat_host::set_error("fat_prefill_paged: the wide prefill kernel runs paged launches on packed copies of K/V "
+                        "only (fp16/bf16, head_dim 128, long chunks, and the workspace of "
+                        "fat_prefill_paged_workspace_bytes)");
+    return FAT_E_UNSUPPORTED;
+  }
+  if (a->workspace && ((uintptr_t)a->workspace & 255)) {
+    fat_host::set_error("fat_prefill_paged: workspace must be 256-byte aligned");
+    return FAT_E_INVALID;
+  }
   if (a->max_seqlen_q == 0 || a->total_q == 0) return FAT_OK;  // nothing to compute
 
   fat::PrefillParams prm{};
@@ -1639,6 +1700,27 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   prm.pshift = __builtin_ctz((unsigned)P);
   prm.num_pages = a->num_pages;
   prm.max_pages = a->max_pages;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const int64_t kv_bound = (int64_t)a->max_pages * P;  // longest context the table can hold
+  if (stage_rows > 0 && a->workspace) {
+    // Packed copies of the used K/V rows, then the packed wide kernel on them.
+    const PagedStageLayout L = paged_stage_layout(a, stage_rows);
+    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+    int32_t* cu_k = reinterpret_cast<int32_t*>(ws);
+    const int rc = fat_host::launch_paged_stage(prm, D, a->batch, (int)kv_bound, cu_k, ws + L.k, ws + L.v, stream);
+    if (rc != FAT_OK) return rc;
+    fat::PrefillParams pk = prm;
+    pk.k = ws + L.k;
+    pk.v = ws + L.v;
+    pk.cu_k = cu_k;
+    pk.k_st = pk.v_st = (int64_t)a->num_kv_heads * D;
+    pk.k_sh = pk.v_sh = D;
+    pk.pt = nullptr;
+    pk.lens = nullptr;
+    return launch_prefill<0>(pk, a->max_seqlen_q, kv_bound, a->dtype, D, a->causal != 0, a->softmax_scale,
+                             FAT_KERNEL_PREFILL_WIDE, "fat_prefill_paged", stream,
+                             L.total > L.vpre ? ws + L.vpre : nullptr, (int)stage_rows, a->total_q);
+  }
   // One load covers 256 / (D / 8) rows (16 at D128, 32 at D64): with pages at
   // least that long its rows share a page and the page id is wave-uniform.
   bool uniform = P >= 256 / (D / 8);
@@ -1653,8 +1735,6 @@ extern "C" int fat_prefill_paged(const fat_prefill_paged_args* a, void* stream_p
   // with 64-bit row addresses (FAT_ROWS_WIDE); all three give identical bits.
   if (a->rows == FAT_ROWS_LANE) uniform = false;
   else if (a->rows == FAT_ROWS_WIDE) off32 = false;
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  const int64_t kv_bound = (int64_t)a->max_pages * P;  // longest context the table can hold
   if (uniform && off32)
     return launch_prefill<3>(prm, a->max_seqlen_q, kv_bound, a->dtype, D, a->causal != 0, a->softmax_scale,
                              a->kernel, "fat_prefill_paged", stream);

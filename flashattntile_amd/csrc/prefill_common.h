@@ -102,4 +102,9 @@ int launch_prefill_wide(const fat::PrefillParams& prm, bool bf16, bool causal, d
 // query rows.
 int launch_prefill_generic(const fat::PrefillParams& prm, int dtype, int D, bool causal, bool paged, dim3 grid,
                            hipStream_t stream);
+// Packed copies of a paged launch's K/V rows (prefill_stage.hip): cu_k
+// [B + 1] from `paged`.lens clamped to `cap`, then every sequence's rows into
+// kdst / vdst as [cu_k[B], Hkv, D] (2-byte elements, head_dim 128).
+int launch_paged_stage(const fat::PrefillParams& paged, int D, int B, int cap, int32_t* cu_k, uint8_t* kdst,
+                       uint8_t* vdst, hipStream_t stream);
 }  // namespace fat_host

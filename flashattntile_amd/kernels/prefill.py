@@ -302,9 +302,16 @@ def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: tor
     pt = cache.page_table if cache.page_table.stride(-1) == 1 else cache.page_table.contiguous()
     sl = cache.seq_lens if cache.seq_lens.is_contiguous() else cache.seq_lens.contiguous()
     cu = cu_seqlens_q if cu_seqlens_q.is_contiguous() else cu_seqlens_q.contiguous()
-    _hip.prefill_paged(q, cache.k_cache, cache.v_cache, pt, sl, cu, out, cache.page_size,
-                       int(max_seqlen_q), bool(causal), float(softmax_scale), kernel=_KERNEL_CODES[kernel],
-                       rows=_ROWS_CODES[rows])
+    a = _hip.prefill_paged_args(q, cache.k_cache, cache.v_cache, pt, sl, cu, out, cache.page_size,
+                                int(max_seqlen_q), bool(causal), float(softmax_scale),
+                                kernel=_KERNEL_CODES[kernel], rows=_ROWS_CODES[rows])
+    # Long chunks run on the packed wide kernel through copies of their K/V
+    # rows: allocate the workspace the library asks for (0 for the others).
+    need = _hip.prefill_paged_workspace_bytes(a)
+    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need else None
+    if ws is not None:
+        a.workspace = ws.data_ptr()
+    _hip.prefill_paged_with_args(a, _hip.current_stream_handle(q.device))
     return out
 
 

@@ -43,7 +43,10 @@
 extern "C" {
 #endif
 
-/* 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
+/* 12: fat_prefill_paged_args.workspace and
+ *     fat_prefill_paged_workspace_bytes: long paged prefill chunks run on
+ *     the wide kernel through packed copies of their K/V rows.
+ * 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
  *     the bf16 V pre-pass scales V per (sequence, KV head);
  *     FAT_KERNEL_PREFILL_WIDE; fp32 prefill and head_dim 16..512
  *     (FAT_KERNEL_PREFILL_GENERIC); decode head_dim 16 and 512 (generic
@@ -54,7 +57,7 @@ extern "C" {
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 11
+#define FAT_ABI_VERSION 12
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -254,7 +257,14 @@ typedef struct fat_prefill_args {
  * a sequence sees key j iff j <= i + (kv_len - q_len).  page_size must be a
  * power of two.  Page ids are clamped to [0, num_pages) and kv_len to
  * max_pages * page_size on the device, so a bad table gives a wrong answer,
- * never an out-of-bounds read.  No workspace.
+ * never an out-of-bounds read.
+ * `workspace` is optional: NULL, or 256-byte aligned and holding
+ * fat_prefill_paged_workspace_bytes(args) bytes.  When that is non-zero
+ * (fp16/bf16, head_dim 128, chunks averaging thousands of queries) the
+ * launch first copies the used K/V rows out of the pages into the workspace
+ * and runs the packed wide kernel on the copies (`rows` then has no
+ * effect); without the workspace it runs the paged kernels.  Same results
+ * up to the kernels' rounding (each within the prefill tolerance).
  */
 typedef struct fat_prefill_paged_args {
   const void* q;
@@ -281,8 +291,10 @@ typedef struct fat_prefill_paged_args {
   int32_t causal;
   int32_t dtype; /* FAT_DTYPE_F16, FAT_DTYPE_BF16 or FAT_DTYPE_F32 */
   float softmax_scale;
-  int32_t kernel; /* FAT_KERNEL_AUTO or a FAT_KERNEL_PREFILL_* (not WIDE) */
+  int32_t kernel; /* FAT_KERNEL_AUTO or a FAT_KERNEL_PREFILL_* (WIDE: with
+                     the staging workspace only)                           */
   int32_t rows;   /* FAT_ROWS_AUTO, _WIDE or _LANE                        */
+  void* workspace; /* optional, see above                                 */
 } fat_prefill_paged_args;
 
 /*
@@ -407,6 +419,12 @@ size_t fat_prefill_varlen_workspace_bytes(const fat_prefill_args* args);
 /* Enqueue varlen prefill on `stream`.
  * Replaces flashattn_tile/kernels/prefill.py:236-326 (see file header). */
 int fat_prefill_varlen(const fat_prefill_args* args, void* stream);
+
+/* Bytes of workspace the paged launch described by `args` would use (its
+ * packed K/V copies and, for bf16, the V pre-pass): 0 when it runs on the
+ * paged kernels.  Reads only sizes, dtype, causal and kernel; no device
+ * access.  No reference counterpart (see fat_prefill_paged). */
+size_t fat_prefill_paged_workspace_bytes(const fat_prefill_paged_args* args);
 
 /* Enqueue paged (chunked) prefill on `stream`.  Extends
  * flashattn_tile/kernels/prefill.py:236-326 to K/V read through the page

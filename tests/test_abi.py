@@ -156,6 +156,52 @@ def test_prefill_argument_errors_are_reported():
     assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "rows" in _err()
 
 
+def _paged_sizes(lens_q, cap, dtype, d=128, h=32, hk=8, page=16, causal=1, kernel=0):
+    p = _hip.PrefillPagedArgs()
+    p.batch, p.total_q, p.num_heads, p.num_kv_heads, p.head_dim = len(lens_q), sum(lens_q), h, hk, d
+    p.page_size, p.max_pages, p.num_pages = page, cap // page, len(lens_q) * cap // page
+    p.max_seqlen_q, p.causal, p.dtype, p.kernel = max(lens_q), causal, dtype, kernel
+    return p
+
+
+def test_paged_prefill_staging_plan():
+    """Which paged launches copy their K/V rows for the wide kernel (no
+    device access: sizes only).  Long chunks at head_dim 128 do (fp16 causal
+    from a mean of 4096 queries, bf16 from 2048, as the packed kernel
+    choice); short chunks after long prefixes, head_dim 64, fp32, forced
+    paged kernels and tables far larger than the queries do not."""
+    lib = _hip.lib()
+    need = lambda p: lib.fat_prefill_paged_workspace_bytes(ctypes.byref(p))  # noqa: E731
+    f16, bf16 = _hip.DT_F16, _hip.DT_BF16
+    kv = 8192 * 8 * 128 * 2
+    assert need(_paged_sizes([8192], 8192, f16)) == 256 + 2 * kv
+    assert need(_paged_sizes([8192], 8192, bf16)) > 3 * kv  # + the V pre-pass's fp16 copy
+    assert need(_paged_sizes([2048] * 4, 2048, bf16)) > 0
+    assert need(_paged_sizes([2048] * 4, 2048, f16)) == 0  # fp16 causal: mean below 4096
+    assert need(_paged_sizes([2048] * 4, 2048, f16, causal=0)) > 0
+    assert need(_paged_sizes([512] * 16, 4096, bf16)) == 0  # chunks of 512 after 3584
+    assert need(_paged_sizes([8192], 8192, f16, d=64)) == 0
+    assert need(_paged_sizes([8192], 8192, _hip.DT_F32)) == 0
+    assert need(_paged_sizes([8192], 8192, f16, kernel=_hip.KERNEL_PREFILL_PINGPONG)) == 0
+    assert need(_paged_sizes([8192], 65536, f16)) == 0  # table capacity 8x the queries
+    assert need(_paged_sizes([100], 128, f16, h=8, hk=2, kernel=_hip.KERNEL_PREFILL_WIDE)) > 0
+
+
+def test_paged_prefill_wide_needs_the_staging_workspace():
+    lib = _hip.lib()
+    p = _paged_sizes([100], 128, _hip.DT_F16, d=64, h=8, hk=2, kernel=_hip.KERNEL_PREFILL_WIDE)
+    for f in ("q", "k_cache", "v_cache", "page_table", "seq_lens", "cu_seqlens_q", "out"):
+        setattr(p, f, 0x1000)
+    p.q_stride_t, p.q_stride_h, p.out_stride_t, p.out_stride_h = 8 * 64, 64, 8 * 64, 64
+    p.k_stride_page, p.k_stride_slot, p.k_stride_head = 16 * 2 * 64, 2 * 64, 64
+    p.v_stride_page, p.v_stride_slot, p.v_stride_head = 16 * 2 * 64, 2 * 64, 64
+    assert lib.fat_prefill_paged(ctypes.byref(p), None) == 2 and "packed copies" in _err()
+    p.head_dim = 128
+    assert lib.fat_prefill_paged(ctypes.byref(p), None) == 2 and "packed copies" in _err()  # no workspace
+    p.workspace = 0x1080
+    assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "256-byte aligned" in _err()
+
+
 def test_prefill_args_block_fields():
     """prefill_args fills the fat_prefill_args block from the tensors
     (addresses, element strides, shape, dtype code, scale, kernel) without a

@@ -141,6 +141,50 @@ def test_paged_prefill_equals_packed_prefill(dtype, kernel):
     assert torch.equal(out_paged, out_packed)
 
 
+# (kv_len, q_len): long chunks, a chunk after a prefix, sequences without
+# new tokens (with and without cached keys).
+STAGED = [(2100, 2100), (1500, 600), (0, 0), (700, 0), (2600, 2047)]
+
+
+@pytest.mark.parametrize("P", [1, 16, 256])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_staged_paged_prefill_matches_oracle(dtype, causal, P, monkeypatch):
+    """Forced onto the wide kernel, a paged launch copies the used K/V rows
+    (through the permuted table; slots past each sequence end are poisoned)
+    into its workspace, computes the sequences' offsets on the device, and
+    runs the packed wide kernel on the copies (bf16: after the V pre-pass)."""
+    from flashattntile_amd import _hip
+
+    force_prefill_knobs(monkeypatch, kernel="wide")
+    label = f"staged paged prefill {dtype} P{P} causal={causal}"
+    print(label, flush=True)
+    lens_k = [c[0] for c in STAGED]
+    lens_q = [c[1] for c in STAGED]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, P, dtype, seed=P + 40)
+    a = _hip.prefill_paged_args(q, cache.k_cache, cache.v_cache, cache.page_table, cache.seq_lens, cu, q,
+                                P, max(lens_q), causal, 128 ** -0.5, kernel=_hip.KERNEL_PREFILL_WIDE)
+    assert _hip.prefill_paged_workspace_bytes(a) > 0
+    out = paged_prefill_attention(q, cache, cu, max(lens_q), causal=causal)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, cache, cu, causal), label=label)
+
+
+def test_staged_paged_prefill_agrees_with_the_paged_kernel():
+    """The same causal bf16 launch staged (wide kernel on the copies) and on
+    the paged ping-pong kernel: both within the tolerance of the oracle, and
+    within twice that of each other."""
+    lens_k, lens_q = [3000, 2200], [3000, 2100]
+    q, cache, cu = _case(lens_k, lens_q, 8, 2, 128, 16, torch.bfloat16, seed=5)
+    staged = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, config={"kernel": "wide"})
+    paged = paged_prefill_attention(q, cache, cu, max(lens_q), causal=True, config={"kernel": "pingpong"})
+    torch.cuda.synchronize()
+    ref = _ref32(q, cache, cu, True)
+    assert_parity(staged, ref, label="staged bf16")
+    assert_parity(paged, ref, label="paged bf16")
+    assert_parity(staged, paged.float(), tol=4e-3, label="staged vs paged")
+
+
 def test_paged_prefill_32k_sequence_first_and_last_rows():
     """One causal fp16 sequence of 32768 tokens (2048 pages of 16, permuted)
     read through the page table: the first and last 256 rows of KV heads 0
