@@ -142,17 +142,6 @@ void prefill_wide_kernel(const PrefillParams p) {
   const int row0 = mb * kWideBM + w * kWideRows;
   const float c = p.scale_log2;
 
-  // Q of the wave's two 32-row blocks: the B operands of S^T = K Q^T.
-  u32x4 qf[2][KS];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int qr = min(row0 + 32 * rb + li, q_len - 1);
-    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
-  }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile loads are outstanding from here on
-
   int hi = kv_len;
   if (CAUSAL) hi = min(kv_len, (mb + 1) * kWideBM + shift);
   const int n_tiles = hi > 0 ? (hi + kWideBN - 1) / kWideBN : 0;
@@ -209,6 +198,19 @@ void prefill_wide_kernel(const PrefillParams p) {
       }
     }
   };
+  // Q of the wave's two 32-row blocks (the B operands of S^T = K Q^T), then
+  // the first tile loads, so that their latencies overlap.  The compiler
+  // waits for the Q loads before their first use; the tile loads, issued
+  // later, only make its in-order vmcnt waits stricter.
+  u32x4 qf[2][KS];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int qr = min(row0 + 32 * rb + li, q_len - 1);
+    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+  }
+  if (n_tiles > 0) issue(0, 0);
   // Wait until this wave's loads of every tile before the most recent issue
   // have landed (`pending`: that issue's my_loads loads may still be in flight).
   auto wait_loads = [&](bool pending) __attribute__((always_inline)) {
@@ -357,8 +359,7 @@ void prefill_wide_kernel(const PrefillParams p) {
     auto stage_wait = [&](int t) __attribute__((always_inline)) {
       if (t + 1 < n_tiles) wait_loads(t + 2 < n_tiles);
     };
-    issue(0, 0);
-    if (grp == 0) {
+    if (grp == 0) {  // tile 0 was issued with the Q loads
       stage(-1, 1);
       stage_wait(-1);
     }
