@@ -51,6 +51,18 @@ constexpr float kDecLazy = 8.0f;
 // fp16/bf16 K/V with at least this many query heads per KV head use the MFMA
 // decode (the `kernel` argument field overrides the choice).
 constexpr int kDecMfmaMinGroup = 8;
+
+// K/V rows are read once per launch: streaming (nontemporal) loads.
+#ifndef FAT_DEC_NT
+#define FAT_DEC_NT 1
+#endif
+__device__ __forceinline__ u32x4 kv_load(const u32x4* p) {
+#if FAT_DEC_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
 #ifndef FAT_DEC_MFMA_8BIT
 #define FAT_DEC_MFMA_8BIT 1
 #endif
@@ -249,8 +261,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
       const int slot = tok & (p.P - 1);
       const uint8_t* kp = p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + kv_head_off_k);
       const uint8_t* vp = p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + kv_head_off_v);
-      R.k[i] = *reinterpret_cast<const u32x4*>(kp);
-      R.v[i] = *reinterpret_cast<const u32x4*>(vp);
+      R.k[i] = kv_load(reinterpret_cast<const u32x4*>(kp));
+      R.v[i] = kv_load(reinterpret_cast<const u32x4*>(vp));
       if constexpr (KV != KV_SAME) {
         R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
         R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
@@ -593,8 +605,8 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
       int phys = first && early && !past ? first_pid[i] : ptrow[rs >> p.log2P];
       phys = min(max(phys, 0), p.num_pages - 1);
       const int slot = min(rs + lrow, t_end - 1) & (p.P - 1);
-      R.k[i] = *reinterpret_cast<const u32x4*>(p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + koff));
-      R.v[i] = *reinterpret_cast<const u32x4*>(p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + voff));
+      R.k[i] = kv_load(reinterpret_cast<const u32x4*>(p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + koff)));
+      R.v[i] = kv_load(reinterpret_cast<const u32x4*>(p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + voff)));
       if constexpr (KV != KV_SAME) {
         R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
         R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];

@@ -105,8 +105,8 @@ __global__ __launch_bounds__(256) void paged_decode_generic_kernel(const DecodeP
       const int phys = min(max(ptrow[lp], 0), p.num_pages - 1);
       const int64_t ko = (int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + (int64_t)kvh * p.k_sh + cc * EPC;
       const int64_t vo = (int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + (int64_t)kvh * p.v_sh + cc * EPC;
-      kr[j] = *reinterpret_cast<const u32x4*>(p.k + EB * ko);
-      vr[j] = *reinterpret_cast<const u32x4*>(p.v + EB * vo);
+      kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.k + EB * ko));  // read once
+      vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.v + EB * vo));
       if constexpr (KV != KV_SAME) {
         ksc[j] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
         vsc[j] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
