@@ -168,7 +168,9 @@ __device__ __forceinline__ void quantize_unit_regs(const uint8_t* src, int64_t s
     raw[i] = u32x4{0u, 0u, 0u, 0u};
     if (c < n) {
       const int slot = c / cpr;
-      raw[i] = *reinterpret_cast<const u32x4*>(src + ES * ((int64_t)slot * s_ss + (c - slot * cpr) * CH));
+      // read once: streaming (nontemporal) load
+      raw[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(src + ES * ((int64_t)slot * s_ss + (c - slot * cpr) * CH)));
     }
   }
   float amax = 0.f;

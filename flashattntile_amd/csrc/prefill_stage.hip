@@ -77,8 +77,8 @@ __global__ __launch_bounds__(256) void paged_stage_kv_kernel(const PrefillParams
     const int64_t ko = (int64_t)page * p.k_sp + (int64_t)slot * p.k_st + (int64_t)h * p.k_sh + 8 * ch;
     const int64_t vo = (int64_t)page * p.v_sp + (int64_t)slot * p.v_st + (int64_t)h * p.v_sh + 8 * ch;
     const int64_t d = ((int64_t)(s0 + key) * p.Hkv + h) * D + 8 * ch;
-    const u32x4 kx = *reinterpret_cast<const u32x4*>(p.k + 2 * ko);
-    const u32x4 vx = *reinterpret_cast<const u32x4*>(p.v + 2 * vo);
+    const u32x4 kx = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.k + 2 * ko));  // read once
+    const u32x4 vx = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.v + 2 * vo));
     *reinterpret_cast<u32x4*>(kdst + 2 * d) = kx;
     *reinterpret_cast<u32x4*>(vdst + 2 * d) = vx;
   }
