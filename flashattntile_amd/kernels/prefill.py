@@ -291,10 +291,15 @@ def _validate_paged(q, cache: PagedKVCache, cu_seqlens_q, causal) -> int:
 
 def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: torch.Tensor, max_seqlen_q: int,
                          causal: bool, softmax_scale: float, out: torch.Tensor | None = None,
-                         kernel: str | None = None, rows: str | None = None) -> torch.Tensor:
+                         kernel: str | None = None, rows: str | None = None,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Enqueue ``fat_prefill_paged`` without validation or synchronisation
     (``kernel`` as for :func:`prefill_launch`; ``rows``: None, ``"wide"`` or
-    ``"lane"``, the row addressing of ``PAGED_CONFIG``)."""
+    ``"lane"``, the row addressing of ``PAGED_CONFIG``).  ``workspace``: a
+    uint8 device buffer of at least ``fat_prefill_paged_workspace_bytes`` of
+    the launch (long chunks copy their K/V rows there for the wide kernel);
+    None or too small allocates one, so a caller that must not allocate
+    (graph capture) passes its own."""
     if q.stride(-1) != 1 or cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
         raise ValueError("q and the cache need a contiguous head_dim axis")
     if out is None:
@@ -308,9 +313,10 @@ def paged_prefill_launch(q: torch.Tensor, cache: PagedKVCache, cu_seqlens_q: tor
     # Long chunks run on the packed wide kernel through copies of their K/V
     # rows: allocate the workspace the library asks for (0 for the others).
     need = _hip.prefill_paged_workspace_bytes(a)
-    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need else None
-    if ws is not None:
-        a.workspace = ws.data_ptr()
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        a.workspace = workspace.data_ptr()
     _hip.prefill_paged_with_args(a, _hip.current_stream_handle(q.device))
     return out
 
