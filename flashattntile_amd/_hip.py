@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 # enum fat_dtype
 DT_F16 = 0
@@ -58,6 +58,7 @@ EXPORTED_SYMBOLS = (
     "fat_prefill_paged",
     "fat_quantize_pages",
     "fat_append_kv",
+    "fat_cache_stats",
 )
 
 _c_i64 = ctypes.c_int64
@@ -254,6 +255,20 @@ class AppendArgs(ctypes.Structure):
     ]
 
 
+class CacheStatsArgs(ctypes.Structure):
+    """Mirror of ``fat_cache_stats_args``."""
+
+    _fields_ = [
+        ("seq_lens", _c_vp),
+        ("page_table", _c_vp),
+        ("page_table_stride", _c_i64),
+        ("batch", _c_i32),
+        ("max_pages", _c_i32),
+        ("page_size", _c_i32),
+        ("out", _c_vp),
+    ]
+
+
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
 _ERROR: str | None = None
@@ -303,6 +318,8 @@ def _load() -> None:
         lib.fat_quantize_pages.argtypes = [ctypes.POINTER(QuantizeArgs), _c_vp]
         lib.fat_append_kv.restype = ctypes.c_int
         lib.fat_append_kv.argtypes = [ctypes.POINTER(AppendArgs), _c_vp]
+        lib.fat_cache_stats.restype = ctypes.c_int
+        lib.fat_cache_stats.argtypes = [ctypes.POINTER(CacheStatsArgs), _c_vp]
         _LIB = lib
 
 
@@ -324,6 +341,29 @@ def lib() -> ctypes.CDLL:
     if _LIB is None:
         raise RuntimeError(f"HIP kernel library unavailable: {_ERROR}")
     return _LIB
+
+
+def cache_stats(seq_lens: torch.Tensor, page_table: torch.Tensor, page_size: int) -> list[int]:
+    """``fat_cache_stats`` on the current stream, then one copy back:
+    ``[min_len, max_len, min_page, max_page, total_pages]`` (the page range
+    over the columns the longest sequence uses; INT32_MAX / INT32_MIN when
+    none).  ``seq_lens`` int32 [B] contiguous, ``page_table`` int32 [B, M]
+    with a contiguous last axis."""
+    out = torch.empty(5, dtype=torch.int64, device=seq_lens.device)
+    a = CacheStatsArgs()
+    a.seq_lens = _ptr(seq_lens)
+    a.page_table = _ptr(page_table)
+    a.page_table_stride = page_table.stride(0)
+    a.batch = seq_lens.shape[0]
+    a.max_pages = page_table.shape[1]
+    a.page_size = int(page_size)
+    a.out = _ptr(out)
+    stream = torch.cuda.current_stream(seq_lens.device)
+    _check(lib().fat_cache_stats(ctypes.byref(a), _c_vp(int(stream.cuda_stream))), "fat_cache_stats")
+    host = torch.empty(5, dtype=torch.int64, pin_memory=True)
+    host.copy_(out, non_blocking=True)
+    stream.synchronize()
+    return host.tolist()
 
 
 def dtype_code(dtype: torch.dtype) -> int:

@@ -18,7 +18,7 @@ REPO = PKG.parent
 LIB_DIR = PKG / "_lib"
 LIB_NAME = "libfat_hip.so"
 SOURCES = ["abi.hip", "decode.hip", "decode_generic.hip", "prefill.hip", "prefill_wide.hip", "prefill_generic.hip",
-           "prefill_stage.hip", "kvwrite.hip"]
+           "prefill_stage.hip", "kvwrite.hip", "validate.hip"]
 ARCH = os.environ.get("FAT_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops is switched off: the kernels use scalar fp32 FMAs only.

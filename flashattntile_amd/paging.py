@@ -99,7 +99,8 @@ def _check_layout(cache: PagedKVCache) -> None:
 
 
 def cache_stats(cache: PagedKVCache, with_total_pages: bool = False) -> tuple[int, ...]:
-    """``(min_len, max_len, min_page, max_page)`` in ONE device->host copy.
+    """``(min_len, max_len, min_page, max_page)`` in ONE device->host copy
+    (ROCm tensors: one ``fat_cache_stats`` launch; otherwise torch reductions).
 
     The page range covers ``page_table[:, :ceil(max_len / page_size)]`` for every
     row, the same entries ``paging.py:123-129`` inspects.  With no cached token
@@ -110,11 +111,20 @@ def cache_stats(cache: PagedKVCache, with_total_pages: bool = False) -> tuple[in
     pt = cache.page_table
     if sl.numel() == 0:
         return (0, 0, 0, -1, 0) if with_total_pages else (0, 0, 0, -1)
+    big = torch.iinfo(torch.int32).max
+    if sl.is_cuda and pt.is_cuda and sl.dtype == torch.int32 and pt.dtype == torch.int32 and \
+            sl.is_contiguous() and pt.dim() == 2 and pt.stride(-1) == 1:
+        from . import _hip
+
+        if _hip.is_loaded():  # one fused launch and one copy back (fat_cache_stats)
+            stats = _hip.cache_stats(sl, pt, cache.page_size)
+            if stats[2] == big:
+                stats[2], stats[3] = 0, -1
+            return tuple(stats) if with_total_pages else tuple(stats[:4])
     max_len = sl.max()
     need = torch.div(max_len + (cache.page_size - 1), cache.page_size, rounding_mode="floor")
     cols = torch.arange(pt.shape[1], device=pt.device)
     used = (cols < need).unsqueeze(0).expand_as(pt)
-    big = torch.iinfo(torch.int32).max
     small = torch.iinfo(torch.int32).min
     if pt.numel():
         min_page = torch.where(used, pt, torch.full_like(pt, big)).min()

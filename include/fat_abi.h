@@ -32,6 +32,9 @@
  *   fat_append_kv          flashattn_tile/paging.py:172-210
  *                          (append_tokens), plus the requantisation of the
  *                          touched pages of an int8/fp8 copy of the cache
+ *   fat_cache_stats        the device reductions of validate_cache,
+ *                          flashattn_tile/paging.py:84-130 (as called by
+ *                          flashattn_tile/kernels/decode.py:503-522)
  */
 #ifndef FAT_ABI_H
 #define FAT_ABI_H
@@ -43,7 +46,8 @@
 extern "C" {
 #endif
 
-/* 12: fat_prefill_paged_args.workspace and
+/* 13: fat_cache_stats (paged-cache validation in one launch).
+ * 12: fat_prefill_paged_args.workspace and
  *     fat_prefill_paged_workspace_bytes: long paged prefill chunks run on
  *     the wide kernel through packed copies of their K/V rows.
  * 11: fat_prefill_varlen_workspace_bytes (the workspace one launch uses);
@@ -57,7 +61,7 @@ extern "C" {
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 12
+#define FAT_ABI_VERSION 13
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -439,6 +443,32 @@ int fat_quantize_pages(const fat_quantize_args* args, void* stream);
 /* Enqueue a one-token-per-sequence append on `stream`.
  * Replaces flashattn_tile/paging.py:172-210 (append_tokens). */
 int fat_append_kv(const fat_append_args* args, void* stream);
+
+/*
+ * The numbers a paged-cache validation checks, in one launch.
+ *   seq_lens   int32 [batch]
+ *   page_table int32 [batch, max_pages] (row stride page_table_stride >= max_pages)
+ *   out        int64 [5], device memory: min(seq_lens), max(seq_lens), the
+ *              min and max of page_table[b, c] over every row b and column
+ *              c < min(ceil(max(seq_lens) / page_size), max_pages) (INT32_MAX
+ *              and INT32_MIN when no column is used), and
+ *              sum_b ceil(max(seq_lens[b], 0) / page_size).
+ */
+typedef struct fat_cache_stats_args {
+  const int32_t* seq_lens;
+  const int32_t* page_table;
+  int64_t page_table_stride;
+  int32_t batch;
+  int32_t max_pages;
+  int32_t page_size;
+  int64_t* out;
+} fat_cache_stats_args;
+
+/* Enqueue the reductions of flashattn_tile/paging.py:84-130 (validate_cache:
+ * seq_lens range, used page-table range) and the page count the decode
+ * partition heuristic needs on `stream`; the caller copies `out` back and
+ * checks it (one device-to-host copy per validation). */
+int fat_cache_stats(const fat_cache_stats_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -202,6 +202,20 @@ def test_paged_prefill_wide_needs_the_staging_workspace():
     assert lib.fat_prefill_paged(ctypes.byref(p), None) == 1 and "256-byte aligned" in _err()
 
 
+def test_cache_stats_argument_errors():
+    """fat_cache_stats rejects missing pointers and inconsistent sizes before
+    any device access."""
+    lib = _hip.lib()
+    assert lib.fat_cache_stats(None, None) == 1
+    a = _hip.CacheStatsArgs()
+    assert lib.fat_cache_stats(ctypes.byref(a), None) == 1 and "NULL" in _err()
+    a.seq_lens, a.page_table, a.out = 0x1000, 0x1000, 0x1000
+    a.batch, a.max_pages, a.page_size, a.page_table_stride = 2, 4, 0, 4
+    assert lib.fat_cache_stats(ctypes.byref(a), None) == 1 and "page_size" in _err()
+    a.page_size, a.page_table_stride = 16, 3
+    assert lib.fat_cache_stats(ctypes.byref(a), None) == 1 and "page_table_stride" in _err()
+
+
 def test_prefill_args_block_fields():
     """prefill_args fills the fat_prefill_args block from the tensors
     (addresses, element strides, shape, dtype code, scale, kernel) without a
