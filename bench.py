@@ -379,11 +379,12 @@ PREFILL_SEQ = 8192
 
 
 def bench_prefill_leg(args, device, name, dtype, seq=PREFILL_SEQ):
-    """One dtype of the prefill leg, timed as the decode headline is: the
-    contract's steps right after the warm-up steps (the main figures and the
-    roofline), then the same steps after SUSTAIN_MS of load (`sustained`)."""
-    steps = max(10, args.steps // 10)
-    warmup = max(3, args.warmup // 4)
+    """One dtype of the prefill leg, timed as the decode headline is, from an
+    idle GPU: exactly --warmup untimed launches, then --steps timed ones (the
+    main figures and the roofline), then the same steps after SUSTAIN_MS of
+    load (`sustained`)."""
+    steps = args.steps
+    warmup = args.warmup
     r = run_prefill([seq], dtype, device, steps, warmup, sustain_ms=SUSTAIN_MS)
     workload = f"prefill_causal_seq{seq}_h32_kv8_d128"
     entry_wl = workload if name == "f16" else f"{workload}_bf16"
