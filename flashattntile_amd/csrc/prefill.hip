@@ -254,9 +254,6 @@ constexpr float kLazy = 8.0f;
 #ifndef FAT_PF_WIDE_MEAN
 #define FAT_PF_WIDE_MEAN 2048
 #endif
-#ifndef FAT_PF_WIDE_MEAN_F16_CAUSAL
-#define FAT_PF_WIDE_MEAN_F16_CAUSAL 4096
-#endif
 #ifndef FAT_PF_SPLIT_MAX
 #define FAT_PF_SPLIT_MAX 256
 #endif
@@ -300,21 +297,24 @@ void prefill_kernel(const PrefillParams p) {
 
   // ---- work item: longest query blocks first; heads sharing a KV head
   // ---- land on the same XCD (consecutive ids go to consecutive XCDs).
+  // Query blocks are counted from each sequence's last row (block jb holds
+  // rows [q_len - 128 (jb + 1), q_len - 128 jb)): a partly empty block is a
+  // sequence's first, with the shortest causal chain.
   const int per = p.B * p.H;
-  const int outer = blockIdx.x / per;
-  const int rem = blockIdx.x - outer * per;
+  const int jb = blockIdx.x / per;
+  const int rem = blockIdx.x - jb * per;
   const int b = rem / p.H;
   const int j = rem - b * p.H;
   const int kvh = j % p.Hkv;
   const int h = kvh * p.group + j / p.Hkv;
-  const int mb = p.nqb - 1 - outer;
 
   const int q_start = p.cu_q[b];
   const int q_len = p.cu_q[b + 1] - q_start;
   constexpr bool PAGED = PG != 0;
   const int k_start = PAGED ? 0 : p.cu_k[b];
   const int kv_len = PAGED ? min(max(p.lens[b], 0), p.max_pages << p.pshift) : p.cu_k[b + 1] - k_start;
-  if (mb * kBM >= q_len) return;  // uniform over the workgroup
+  if (jb * kBM >= q_len) return;  // uniform over the workgroup
+  const int r_end = q_len - jb * kBM;  // one past the block's last row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -324,15 +324,14 @@ void prefill_kernel(const PrefillParams p) {
   const int g = lane >> 5;   // k-group of the MFMA operands
   const int li = lane & 31;  // query column of this lane
   const int shift = kv_len - q_len;
-  const int row0 = mb * kBM + w * 32;  // first query row of this wave
-  const int my_row = row0 + li;
+  const int row0 = r_end - kBM + w * 32;  // first query row of this wave (< 0: not stored)
+  const int my_row = max(row0 + li, 0);   // rows below 0 compute as row 0
   const float c = p.scale_log2;
 
   // Q^T operand (B of S^T = K Q^T): lane holds Q[my_row][16 ks + 8 g + 0..7].
   u32x4 qf[KS];
   {
-    const int qr = min(my_row, q_len - 1);
-    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
+    const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + my_row) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
   }
@@ -342,7 +341,7 @@ void prefill_kernel(const PrefillParams p) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched
 
   int hi = kv_len;
-  if (CAUSAL) hi = min(kv_len, (mb + 1) * kBM + shift);
+  if (CAUSAL) hi = min(kv_len, r_end + shift);
   const int n_all = hi > 0 ? (hi + kBN - 1) / kBN : 0;
   // Steps per group (the same for every group, so barriers pair up); step i
   // of group g is tile g + NG i.  With NG = 2 and n_all odd, group 1's last
@@ -751,21 +750,25 @@ void prefill_pp_kernel(const PrefillParams p) {
   static_assert(!VPRE || (VH && PG == 0), "V pre-conversion is for packed bf16 prefill");
   __shared__ __attribute__((aligned(16))) int vsc[2][4];
 
+  // Query blocks are counted from each sequence's last row (block jb holds
+  // rows [q_len - 256 (jb + 1), q_len - 256 jb)), so a sequence's partly
+  // empty block is its first, whose causal chain is the shortest; the grid
+  // runs jb = 0 (every sequence's longest chain) first.
   const int per = p.B * p.H;
-  const int outer = blockIdx.x / per;
-  const int rem = blockIdx.x - outer * per;
+  const int jb = blockIdx.x / per;
+  const int rem = blockIdx.x - jb * per;
   const int b = rem / p.H;
   const int j = rem - b * p.H;
   const int kvh = j % p.Hkv;
   const int h = kvh * p.group + j / p.Hkv;
-  const int mb = p.nqb - 1 - outer;
 
   const int q_start = p.cu_q[b];
   const int q_len = p.cu_q[b + 1] - q_start;
   constexpr bool PAGED = PG != 0;
   const int k_start = PAGED ? 0 : p.cu_k[b];
   const int kv_len = PAGED ? min(max(p.lens[b], 0), p.max_pages << p.pshift) : p.cu_k[b + 1] - k_start;
-  if (mb * kPBM >= q_len) return;  // uniform over the workgroup
+  if (jb * kPBM >= q_len) return;  // uniform over the workgroup
+  const int r_end = q_len - jb * kPBM;  // one past the block's last row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -775,13 +778,16 @@ void prefill_pp_kernel(const PrefillParams p) {
   const int g = lane >> 5;
   const int li = lane & 31;
   const int shift = kv_len - q_len;
-  const int row0 = mb * kPBM + w * 32;
-  const int my_row = row0 + li;
+  // The wave's first row; negative in a sequence's first block when q_len is
+  // not a multiple of 256.  Rows below 0 compute as row 0 (my_row) and are
+  // not stored.
+  const int row0 = r_end - kPBM + w * 32;
+  const int my_row = max(row0 + li, 0);
   const float c = p.scale_log2;
 
   u32x4 qf[KS];
   {
-    const int qr = min(my_row, q_len - 1);
+    const int qr = my_row;
     const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
@@ -789,7 +795,7 @@ void prefill_pp_kernel(const PrefillParams p) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): retire the Q loads before the loop
 
   int hi = kv_len;
-  if (CAUSAL) hi = min(kv_len, (mb + 1) * kPBM + shift);
+  if (CAUSAL) hi = min(kv_len, r_end + shift);
   const int n_tiles = hi > 0 ? (hi + kBN - 1) / kBN : 0;
 
   f32x16 acc[DB];
@@ -1027,10 +1033,10 @@ void prefill_pp_kernel(const PrefillParams p) {
     // Causal: tiles past this wave's last visible key are fully masked for
     // it; from tile nv on the wave only stages tiles and keeps the barrier
     // count (two per tile) of the rest of the workgroup.  A wave whose rows
-    // all lie past the sequence's last query (the last block of a sequence
-    // whose length is not a multiple of 256) stops after tile 0: nothing it
-    // computes is stored.
-    const int nv = row0 >= q_len ? 1 : CAUSAL ? min(n_tiles, (row0 + 31 + shift) / kBN + 1) : n_tiles;
+    // all lie before the sequence's first query (the first block of a
+    // sequence whose length is not a multiple of 256) stops after tile 0:
+    // nothing it computes is stored.
+    const int nv = row0 + 32 <= 0 ? 1 : CAUSAL ? min(n_tiles, (row0 + 31 + shift) / kBN + 1) : n_tiles;
     for (int t = 1; t < nv; ++t) {
       // sched_barrier keeps every instruction inside its phase (the compiler
       // would otherwise move MFMAs across the workgroup barrier); the MFMA
@@ -1311,14 +1317,15 @@ PrefillKind choose_prefill_kind(int64_t B, int64_t H, int max_seqlen_q, int64_t 
   // The 64-rows-per-wave kernel once its 512-row blocks alone cover the CUs
   // (causal grids: more than that, as for the ping-pong kernel), for packed
   // fp16 at head_dim 128, and bf16 whose V the pre-pass converts, when the
-  // sequences are long on average: a sequence's last block is partly empty,
-  // and a 512-row block with one working wave takes as long as a full one.
-  // Measured (32/8 heads, D128, one box): fp16 causal gains 5 % at L8192,
-  // breaks even at 4 x 4096 and loses 3 % on the mixed pack of 8 (mean 2435
-  // queries); bf16 and non-causal gain from a mean of 2048.
-  const int64_t wide_mean = (dtype == FAT_DTYPE_F16 && causal) ? FAT_PF_WIDE_MEAN_F16_CAUSAL : FAT_PF_WIDE_MEAN;
+  // sequences average at least FAT_PF_WIDE_MEAN queries: a sequence's partly
+  // empty block (its first) costs a 512-row block's chain.  Measured (32/8
+  // heads, D128, one box, fp16 causal against the ping-pong kernel): 5 %
+  // faster at L8192, 1-3 % on packs of 8 or 16 sequences drawn from
+  // [1, 4096] (means 1950-2500), level at 8 x 2048, 7-8 % slower at means
+  // near 1000; bf16 and non-causal gain from a mean of 2048.
   if (kind == PF_PINGPONG && packed && D == 128 && (dtype == FAT_DTYPE_F16 || vpre_ok) &&
-      (causal ? n_wide > FAT_PF_WIDE_MIN_CAUSAL : n_wide >= FAT_PF_WIDE_MIN_FULL) && total_q >= wide_mean * B)
+      (causal ? n_wide > FAT_PF_WIDE_MIN_CAUSAL : n_wide >= FAT_PF_WIDE_MIN_FULL) &&
+      total_q >= FAT_PF_WIDE_MEAN * B)
     kind = PF_WIDE;
   if (kernel != FAT_KERNEL_AUTO) {
     kind = kernel == FAT_KERNEL_PREFILL_PINGPONG ? PF_PINGPONG
@@ -1434,7 +1441,14 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
     prm.v_sh = D;
     prm.v_head_scale = seq_scale;
   }
-  if (kind == PF_WIDE) return fat_host::launch_prefill_wide(prm, dtype == FAT_DTYPE_BF16, causal, grid, stream);
+  if (kind == PF_WIDE) {
+    // Packs of 2-16 sequences run their (query block, sequence) items
+    // longest chain first (the kernel ranks them: O(B) per thread, at most
+    // 512 items, one per thread).
+    const int64_t items = (int64_t)prm.nqb * prm.B;
+    prm.rank_items = (prm.B >= 2 && prm.B <= fat::kWideRankMaxSeqs && items <= fat::kWideBM) ? (int)items : 0;
+    return fat_host::launch_prefill_wide(prm, dtype == FAT_DTYPE_BF16, causal, grid, stream);
+  }
   if (dtype == FAT_DTYPE_F16) return launch_prefill_d<fat::F16, PG>(prm, D, causal, kind, grid, stream);
   return launch_prefill_d<fat::BF16, PG>(prm, D, causal, kind, grid, stream);
 }
@@ -1552,11 +1566,18 @@ extern "C" int fat_prefill_varlen(const fat_prefill_args* a, void* stream_ptr) {
 // launch runs on the wide kernel through them, else 0.  Taken when the packed
 // launch of the same shape would run the wide kernel (fp16, or bf16 whose
 // copied V the pre-pass converts; head_dim 128; sequences averaging
-// FAT_PF_WIDE_MEAN queries or more, choose_prefill_kind), when the copies
-// hold at most 4 rows per query (the workspace stays in proportion to the
-// launch) and fit the packed kernels' 32-bit offsets.  The copies cost one
-// read and one write of the used K/V rows; the wide kernel then reads each
-// row once per query block, 16 bytes a lane straight into LDS.
+// FAT_PF_WIDE_MEAN queries or more, choose_prefill_kind; fp16 causal
+// launches FAT_PF_STAGE_MEAN_F16_CAUSAL unless the wide kernel is asked
+// for, since there the wide kernel gains
+// least over the paged ping-pong kernel and the copies cost the same), when
+// the copies hold at most 4 rows per query (the workspace stays in
+// proportion to the launch) and fit the packed kernels' 32-bit offsets.  The
+// copies cost one read and one write of the used K/V rows; the wide kernel
+// then reads each row once per query block, 16 bytes a lane straight into
+// LDS.
+#ifndef FAT_PF_STAGE_MEAN_F16_CAUSAL
+#define FAT_PF_STAGE_MEAN_F16_CAUSAL 4096
+#endif
 int64_t paged_stage_rows(const fat_prefill_paged_args* a) {
   if (a->head_dim != 128 || (a->dtype != FAT_DTYPE_F16 && a->dtype != FAT_DTYPE_BF16)) return 0;
   if (a->kernel != FAT_KERNEL_AUTO && a->kernel != FAT_KERNEL_PREFILL_WIDE) return 0;
@@ -1568,6 +1589,9 @@ int64_t paged_stage_rows(const fat_prefill_paged_args* a) {
   if (rows > 4 * (int64_t)a->total_q || rows * a->num_kv_heads * a->head_dim * 2 >= 0x7fffffffLL) return 0;
   const bool fits = vpre_fits(a->batch, a->num_kv_heads, a->head_dim, rows, cap);
   if (a->dtype == FAT_DTYPE_BF16 && !fits) return 0;
+  if (a->kernel == FAT_KERNEL_AUTO && a->dtype == FAT_DTYPE_F16 && a->causal &&
+      a->total_q < (int64_t)FAT_PF_STAGE_MEAN_F16_CAUSAL * a->batch)
+    return 0;
   const PrefillKind kind = choose_prefill_kind(a->batch, a->num_heads, a->max_seqlen_q, cap, a->causal != 0,
                                                a->kernel, a->head_dim, a->dtype, true, fits, a->total_q);
   return kind == PF_WIDE ? rows : 0;

@@ -28,11 +28,19 @@ struct PrefillParams {
   // bf16 V converted ahead of the kernel (VPRE instantiations): v points at
   // fp16 values scaled by 2^-v_head_scale[sequence * Hkv + kv head].
   const int32_t* v_head_scale;
+  // Wide kernel: > 0 when the launch's nqb * B work items (query block,
+  // sequence) run longest causal chain first (ranked on the device); 0: in
+  // block order.
+  int32_t rank_items;
 };
 
 constexpr int kBM = 128;
 // Query rows per workgroup of the 64-rows-per-wave kernel (prefill_wide.hip).
 constexpr int kWideBM = 512;
+// Most sequences a wide launch ranks its work items over (the ranking costs
+// each thread a loop over the sequences; one item per thread, so at most
+// kWideBM items).
+constexpr int kWideRankMaxSeqs = 16;
 constexpr int kBN = 64;
 // Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
 constexpr int kBufFlags = 0x00020000;
@@ -77,7 +85,7 @@ __device__ __forceinline__ void write_rows_via_lds(uint16_t* ob, int li, int g, 
   for (int i = 0; i < 32 / RPI; ++i) {
     const int r = i * RPI + orow;
     const u32x4 val = *reinterpret_cast<const u32x4*>(&ob[r * OS + 8 * oc]);
-    if (row0 + r < q_len) {
+    if ((unsigned)(row0 + r) < (unsigned)q_len) {  // rows in [0, q_len)
       uint8_t* dst = p.out + 2 * ((int64_t)(q_start + row0 + r) * p.o_st + (int64_t)h * p.o_sh + 8 * oc);
       if (o16) {
         *reinterpret_cast<u32x4*>(dst) = val;

@@ -104,6 +104,54 @@ __device__ __forceinline__ void buffer_load_lds16(const i32x4& desc, int voff, i
       : "memory", "m0");
 }
 
+// Longest-first order of a packed launch's work items.  Item i = (query
+// block jb = i / B counted from the sequence's end, sequence b = i % B); its
+// causal chain holds kv_len - 512 jb keys (kv_len when not causal).  Items
+// are ordered by chain length (descending), then sequence, then block; items
+// without query rows come last.  Each thread ranks one item with a count per
+// sequence (a sequence's chains form an arithmetic progression), O(B) work,
+// and the workgroup takes the item of rank `target`, or -1 (no rows: the
+// workgroup exits).  Needs B * nqb <= blockDim.x and a 2 B + 1 int LDS area;
+// every thread of the workgroup calls it.
+template <bool CAUSAL>
+__device__ __forceinline__ int wide_ranked_item(const PrefillParams& p, int n, int target, int* s_len) {
+  constexpr int BM = kWideBM;
+  const int t = threadIdx.x;
+  const int B = p.B;
+  if (t < B) {
+    s_len[2 * t] = p.cu_q[t + 1] - p.cu_q[t];
+    s_len[2 * t + 1] = p.cu_k[t + 1] - p.cu_k[t];
+  }
+  if (t == 0) s_len[2 * B] = -1;
+  __syncthreads();
+  if (t < n) {
+    const int tb = t % B;
+    const int tj = t / B;
+    if (tj * BM < s_len[2 * tb]) {  // the item has query rows
+      const int kl = s_len[2 * tb + 1];
+      const int X = CAUSAL ? kl - tj * BM : kl;
+      int rank = 0;
+      for (int b2 = 0; b2 < B; ++b2) {
+        const int nb2 = (max(s_len[2 * b2], 0) + BM - 1) / BM;  // items of b2 with rows
+        const int kl2 = s_len[2 * b2 + 1];
+        if (CAUSAL) {
+          // b2's block j2 has chain kl2 - j2 BM: longer than X for j2 < d / BM.
+          const int d = kl2 - X;
+          rank += d > 0 ? min((d + BM - 1) / BM, nb2) : 0;
+          // an equal chain (j2 = d / BM) comes first when b2 < tb
+          if (b2 < tb && d >= 0 && d % BM == 0 && d / BM < nb2) ++rank;
+        } else {
+          if (kl2 > X || (kl2 == X && b2 < tb)) rank += nb2;
+          else if (kl2 == X && b2 == tb) rank += tj;
+        }
+      }
+      if (rank == target) s_len[2 * B] = t;
+    }
+  }
+  __syncthreads();
+  return s_len[2 * B];
+}
+
 template <typename T, bool CAUSAL, bool POS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_wide_kernel(const PrefillParams p) {
@@ -116,20 +164,30 @@ void prefill_wide_kernel(const PrefillParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[8 * kOutStage<D> * 2];
   static_assert(kWideBufs * (kKTile + kVTile) <= (int)sizeof(lds), "tiles");
 
-  const int per = p.B * p.H;
-  const int outer = blockIdx.x / per;
-  const int rem = blockIdx.x - outer * per;
-  const int b = rem / p.H;
-  const int j = rem - b * p.H;
+  // Query blocks are counted from each sequence's last row (block jb holds
+  // rows [q_len - 512 (jb + 1), q_len - 512 jb)), so a sequence's partly
+  // empty block is its first, whose causal chain is the shortest.  The grid
+  // runs item (jb, b) = blockIdx.x / H, jb-major (every sequence's longest
+  // chain first), or, with rank_items, the items longest chain first
+  // (wide_ranked_item); the H query heads of an item are consecutive.
+  __shared__ int s_items[2 * kWideRankMaxSeqs + 1];
+  int item = blockIdx.x / p.H;
+  const int j = blockIdx.x - item * p.H;
+  if (p.rank_items > 0) {
+    item = wide_ranked_item<CAUSAL>(p, p.rank_items, item, s_items);
+    if (item < 0) return;  // uniform: no item of this rank has rows
+  }
+  const int jb = item / p.B;
+  const int b = item - jb * p.B;
   const int kvh = j % p.Hkv;
   const int h = kvh * p.group + j / p.Hkv;
-  const int mb = p.nqb - 1 - outer;
 
   const int q_start = p.cu_q[b];
   const int q_len = p.cu_q[b + 1] - q_start;
   const int k_start = p.cu_k[b];
   const int kv_len = p.cu_k[b + 1] - k_start;
-  if (mb * kWideBM >= q_len) return;  // uniform over the workgroup
+  if (jb * kWideBM >= q_len) return;  // uniform over the workgroup
+  const int r_end = q_len - jb * kWideBM;  // one past the block's last row
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -139,11 +197,13 @@ void prefill_wide_kernel(const PrefillParams p) {
   const int g = lane >> 5;
   const int li = lane & 31;
   const int shift = kv_len - q_len;
-  const int row0 = mb * kWideBM + w * kWideRows;
+  // The wave's first row; negative in a sequence's first block when q_len is
+  // not a multiple of 512 (rows below 0 compute as row 0 and are not stored).
+  const int row0 = r_end - kWideBM + w * kWideRows;
   const float c = p.scale_log2;
 
   int hi = kv_len;
-  if (CAUSAL) hi = min(kv_len, (mb + 1) * kWideBM + shift);
+  if (CAUSAL) hi = min(kv_len, r_end + shift);
   const int n_tiles = hi > 0 ? (hi + kWideBN - 1) / kWideBN : 0;
 
   f32x16 acc[2][DB];
@@ -205,7 +265,7 @@ void prefill_wide_kernel(const PrefillParams p) {
   u32x4 qf[2][KS];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    const int qr = min(row0 + 32 * rb + li, q_len - 1);
+    const int qr = max(row0 + 32 * rb + li, 0);
     const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
@@ -282,7 +342,7 @@ void prefill_wide_kernel(const PrefillParams p) {
       // compiler from holding 16 per-lane key indices across the loop).
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const int lim = CAUSAL ? min(kv_len - 1, row0 + 32 * rb + li + shift) : kv_len - 1;
+        const int lim = CAUSAL ? min(kv_len - 1, max(row0 + 32 * rb + li, 0) + shift) : kv_len - 1;
         const int rel = lim - n0 - 4 * g;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[rb][r] = ((r & 3) + 8 * (r >> 2)) <= rel ? s[rb][r] : -INFINITY;
@@ -376,11 +436,11 @@ void prefill_wide_kernel(const PrefillParams p) {
     stage_wait(0);
     // Causal: tiles past this wave's last visible key are fully masked for
     // it; from tile nv on the wave only loads tiles and keeps the barrier
-    // count.  A wave whose rows all lie past the sequence's last query stops
-    // computing after tile 0 (nothing it computes is stored).
-    const int nv = row0 >= q_len ? 1
-                   : CAUSAL      ? min(n_tiles, (row0 + kWideRows - 1 + shift) / kWideBN + 1)
-                                 : n_tiles;
+    // count.  A wave whose rows all lie before the sequence's first query
+    // stops computing after tile 0 (nothing it computes is stored).
+    const int nv = row0 + kWideRows <= 0 ? 1
+                   : CAUSAL          ? min(n_tiles, (row0 + kWideRows - 1 + shift) / kWideBN + 1)
+                                     : n_tiles;
     int bk = 1;  // t % 3 for the loop's t
     for (int t = 1; t < nv; ++t) {
       const int bprev = bk == 0 ? 2 : bk - 1;  // (t - 1) % 3 == (t + 2) % 3

@@ -164,6 +164,37 @@ def test_prefill_kv_longer_than_q(dtype, causal, kernel):
     assert_parity(out, _ref32(q, k, v, cq, ck, causal, scale=0.07), label=label)
 
 
+def _wide_pack(n, seed):
+    """n (kv_len, q_len) pairs: queries of 1-1300 tokens, some after a prefix
+    of up to 700 keys, a few without queries."""
+    g = torch.Generator().manual_seed(seed)
+    pairs = []
+    for i in range(n):
+        lq = int(torch.randint(1, 1301, (1,), generator=g))
+        pre = int(torch.randint(0, 701, (1,), generator=g)) if i % 3 == 1 else 0
+        if i % 7 == 5:
+            lq = 0
+        pairs.append((lq + pre, lq))
+    return pairs
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("n", [2, 16, 17, 40])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_wide_kernel_pack_orders(dtype, n, causal):
+    """The wide kernel runs packs of 2-16 sequences in an order it ranks on
+    the device (longest causal chain first) and larger packs in block order;
+    either way every (query block, sequence) item is computed once.  Ragged
+    packs on both sides of that limit, with prefixes and sequences without
+    queries, against the oracle."""
+    label = f"prefill wide pack of {n} {dtype} causal={causal}"
+    print(label, flush=True)
+    q, k, v, cq, ck, mq, mk = _varlen_kq(_wide_pack(n, seed=n), 8, 2, 128, dtype, seed=n + 1)
+    out = prefill_attention(q, k, v, cq, ck, mq, mk, causal=causal, config={"kernel": "wide"})
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, k, v, cq, ck, causal), label=label)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_prefill_mixed_pack_baseline(dtype, kernel):
     """BASELINE configs[2] mixed pack: 8 sequences, lengths uniform in [1, 4096]."""
