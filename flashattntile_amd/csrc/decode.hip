@@ -56,12 +56,13 @@ constexpr int kDecMfmaMinGroup = 8;
 #ifndef FAT_DEC_NT
 #define FAT_DEC_NT 1
 #endif
-__device__ __forceinline__ u32x4 kv_load(const u32x4* p) {
-#if FAT_DEC_NT
-  return __builtin_nontemporal_load(p);
-#else
-  return *p;
-#endif
+// 16 bytes of K or V at base + off through a raw buffer descriptor of range
+// `bytes` (offsets at or past it read as zeros); base is wave-uniform (a
+// page's row), off the lane's chunk.  Cache policy 2 is the nt (streaming)
+// bit of gfx950 loads.
+__device__ __forceinline__ u32x4 kv_buffer_load(const uint8_t* base, int bytes, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kBufFlags);
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, FAT_DEC_NT ? 2 : 0));
 }
 #ifndef FAT_DEC_MFMA_8BIT
 #define FAT_DEC_MFMA_8BIT 1
@@ -243,26 +244,40 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     }
   }
 
-  const int64_t kv_head_off_k = (int64_t)kvh * p.k_sh + c * EPL;
-  const int64_t kv_head_off_v = (int64_t)kvh * p.v_sh + c * EPL;
   constexpr int EB = Gm::kElemBytes;
+  // Load i of a unit covers rows rs .. rs + RPL - 1 of one page (page_size
+  // >= RPL, rs a multiple of RPL): its address is wave-uniform (page id,
+  // slot and KV head on the scalar unit, in a buffer descriptor) plus this
+  // lane's loop-invariant offset (row r, chunk c).  The descriptor's range
+  // ends with the partition's last row, so rows past t_end (and loads wholly
+  // past it) read as zeros: their scores are masked, and zero V rows keep
+  // p * v = 0.
+  // Byte strides (the host keeps a page below 4 GB and RPL rows below 2 GB).
+  const uint8_t* const kh = p.k + (int64_t)EB * kvh * p.k_sh;  // this KV head's slice of page 0
+  const uint8_t* const vh = p.v + (int64_t)EB * kvh * p.v_sh;
+  const uint32_t kpage = (uint32_t)(EB * p.k_sp), vpage = (uint32_t)(EB * p.v_sp);
+  const uint32_t krow = (uint32_t)(EB * p.k_ss), vrow = (uint32_t)(EB * p.v_ss);
+  const uint32_t lane_k = r * krow + EB * EPL * c;
+  const uint32_t lane_v = r * vrow + EB * EPL * c;
 
   // first: u is this wave's first unit (first_pid holds its page ids).
   auto fetch = [&](UnitRegs<NI>& R, int u, bool first) {
     const int base = t_begin + (u << UL);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      int rs = base + i * RPL;
-      const bool past = rs >= t_end;
-      if (past) rs = (t_end - 1) & ~(RPL - 1);
-      int phys = first && early && !past ? first_pid[i] : ptrow[rs >> p.log2P];
-      phys = min(max(phys, 0), p.num_pages - 1);
-      const int tok = min(rs + r, t_end - 1);
-      const int slot = tok & (p.P - 1);
-      const uint8_t* kp = p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + kv_head_off_k);
-      const uint8_t* vp = p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + kv_head_off_v);
-      R.k[i] = kv_load(reinterpret_cast<const u32x4*>(kp));
-      R.v[i] = kv_load(reinterpret_cast<const u32x4*>(vp));
+      const int rs = base + i * RPL;
+      const int nrow = min(t_end - rs, RPL);  // rows of this load in the partition
+      // The table is read without a branch (at most its last entry) so that
+      // a unit's page-id loads issue together; a load wholly past t_end reads
+      // nothing (range 0).
+      int phys = first && early ? first_pid[i] : ptrow[min(rs >> p.log2P, p.max_pages - 1)];
+      phys = __builtin_amdgcn_readfirstlane(min(max(phys, 0), p.num_pages - 1));
+      const uint32_t slot0 = (uint32_t)(rs & (p.P - 1));
+      // range: the load's rows inside the partition, each up to its head slice's end
+      const int nk = nrow > 0 ? (int)((uint32_t)(nrow - 1) * krow + EB * D) : 0;
+      const int nv = nrow > 0 ? (int)((uint32_t)(nrow - 1) * vrow + EB * D) : 0;
+      R.k[i] = kv_buffer_load(kh + (uint64_t)(uint32_t)phys * kpage + slot0 * krow, nk, lane_k);
+      R.v[i] = kv_buffer_load(vh + (uint64_t)(uint32_t)phys * vpage + slot0 * vrow, nv, lane_v);
       if constexpr (KV != KV_SAME) {
         R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
         R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
@@ -305,12 +320,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
 
-  UnitRegs<NI> nxt;
-  if (w < n_units) fetch(nxt, w, true);
-
-  for (int u = w; u < n_units; u += NW) {
-    const UnitRegs<NI> cur = nxt;
-    if (u + NW < n_units) fetch(nxt, u + NW, false);
+  // One unit: scores, online softmax, PV.
+  auto process = [&](const UnitRegs<NI>& cur, int u) __attribute__((always_inline)) {
     const int base = t_begin + (u << UL);
 
     // ---- scores: partial q.k over this lane's EPL dims ----
@@ -436,6 +447,16 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
         for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(pg, vf[e], acc[g][e]);
       }
     }
+  };
+
+  // Two register sets, unit u + NW loading while unit u is processed (the
+  // loop is unrolled by two so that no copy moves one set into the other).
+  UnitRegs<NI> nxt;
+  if (w < n_units) fetch(nxt, w, true);
+  for (int u = w; u < n_units; u += NW) {
+    const UnitRegs<NI> cur = nxt;
+    if (u + NW < n_units) fetch(nxt, u + NW, false);
+    process(cur, u);
   }
 
   // ---- merge rows of the wave (same m), then the waves of the workgroup ----
@@ -584,12 +605,19 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
 
   const int lrow = lane / CPR;  // this lane's row inside each load
   const int lcol = lane % CPR;  // and its 16-byte chunk
-  const int64_t koff = (int64_t)kvh * p.k_sh + lcol * EPC;
-  const int64_t voff = (int64_t)kvh * p.v_sh + lcol * EPC;
   // Raw K/V chunks of a 32-key block: load i covers rows RPL*i .. RPL*i +
   // RPL - 1, which lie in one page (page_size >= RPL), so its page id and
-  // (8-bit caches) scales are wave-uniform.  Rows past t_end re-read the last
-  // valid key; their scores are masked.
+  // (8-bit caches) scales are wave-uniform.  Its address is that page's
+  // base (scalar unit, in a buffer descriptor) plus this lane's
+  // loop-invariant offset; the descriptor's range ends with the partition's
+  // last row, so rows past t_end read as zeros (their scores are masked, and
+  // zero bytes are zero in every cache type).
+  const uint8_t* const kh = p.k + (int64_t)EB * kvh * p.k_sh;  // this KV head's slice of page 0
+  const uint8_t* const vh = p.v + (int64_t)EB * kvh * p.v_sh;
+  const uint32_t kpage = (uint32_t)(EB * p.k_sp), vpage = (uint32_t)(EB * p.v_sp);
+  const uint32_t krow = (uint32_t)(EB * p.k_ss), vrow = (uint32_t)(EB * p.v_ss);
+  const uint32_t lane_k = lrow * krow + 16 * lcol;
+  const uint32_t lane_v = lrow * vrow + 16 * lcol;
   struct Raw {
     u32x4 k[NLD], v[NLD];
     float ksc[NLD], vsc[NLD];
@@ -599,14 +627,17 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
     const int kb = t_begin + (blk << 5);
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
-      int rs = kb + i * RPL;
-      const bool past = rs >= t_end;
-      if (past) rs = (t_end - 1) & ~(RPL - 1);
-      int phys = first && early && !past ? first_pid[i] : ptrow[rs >> p.log2P];
-      phys = min(max(phys, 0), p.num_pages - 1);
-      const int slot = min(rs + lrow, t_end - 1) & (p.P - 1);
-      R.k[i] = kv_load(reinterpret_cast<const u32x4*>(p.k + EB * ((int64_t)phys * p.k_sp + (int64_t)slot * p.k_ss + koff)));
-      R.v[i] = kv_load(reinterpret_cast<const u32x4*>(p.v + EB * ((int64_t)phys * p.v_sp + (int64_t)slot * p.v_ss + voff)));
+      const int rs = kb + i * RPL;
+      const int nrow = min(t_end - rs, RPL);  // rows of this load in the partition
+      // read without a branch (at most the table's last entry); a load wholly
+      // past t_end reads nothing (range 0)
+      int phys = first && early ? first_pid[i] : ptrow[min(rs >> p.log2P, p.max_pages - 1)];
+      phys = __builtin_amdgcn_readfirstlane(min(max(phys, 0), p.num_pages - 1));
+      const uint32_t slot0 = (uint32_t)(rs & (p.P - 1));
+      const int nk = nrow > 0 ? (int)((uint32_t)(nrow - 1) * krow + EB * D) : 0;
+      const int nv = nrow > 0 ? (int)((uint32_t)(nrow - 1) * vrow + EB * D) : 0;
+      R.k[i] = kv_buffer_load(kh + (uint64_t)(uint32_t)phys * kpage + slot0 * krow, nk, lane_k);
+      R.v[i] = kv_buffer_load(vh + (uint64_t)(uint32_t)phys * vpage + slot0 * vrow, nv, lane_v);
       if constexpr (KV != KV_SAME) {
         R.ksc[i] = p.ks[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
         R.vsc[i] = p.vs[(int64_t)phys * p.sc_sp + (int64_t)kvh * p.sc_sh];
@@ -1064,13 +1095,22 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   // power-of-two pages of at least the rows one 16-byte load per lane covers
   // (their loads read one page id per load); the generic kernel takes the rest.
   const int rpl = (kv == fat::KV_SAME) ? (D == 128 ? 4 : 8) : (D == 128 ? 8 : 16);
-  const bool fast_ok = a->q_dtype != FAT_DTYPE_F32 && (D == 64 || D == 128) && log2P >= 0 && a->page_size >= rpl;
+  // They address K/V through 32-bit byte offsets from a page's base: strides
+  // non-negative, a page below 4 GB, the rows of one 32-key block below 2 GB.
+  const int64_t kv_eb = (kv == fat::KV_SAME) ? (a->q_dtype == FAT_DTYPE_F32 ? 4 : 2) : 1;
+  auto fits32 = [&](int64_t sp, int64_t ss, int64_t sh) {
+    return sp >= 0 && ss >= 0 && sh >= 0 && kv_eb * sp < (int64_t(1) << 32) && kv_eb * (32 * ss + D) < (int64_t(1) << 31);
+  };
+  const bool strides_ok = fits32(a->k_stride_page, a->k_stride_slot, a->k_stride_head) &&
+                          fits32(a->v_stride_page, a->v_stride_slot, a->v_stride_head);
+  const bool fast_ok = a->q_dtype != FAT_DTYPE_F32 && (D == 64 || D == 128) && log2P >= 0 && a->page_size >= rpl &&
+                       strides_ok;
   const bool generic = a->kernel == FAT_KERNEL_DECODE_GENERIC || (a->kernel == FAT_KERNEL_AUTO && !fast_ok);
   if (!generic && !fast_ok) {
-    fat_host::set_error("fat_paged_decode: the %s decode kernel takes fp16/bf16 queries, head_dim 64 or 128 and "
-                        "power-of-two pages of at least %d rows (page_size %d, head_dim %d); use "
-                        "FAT_KERNEL_AUTO or FAT_KERNEL_DECODE_GENERIC", a->kernel == FAT_KERNEL_DECODE_VALU ? "VALU"
-                        : "MFMA", rpl, a->page_size, D);
+    fat_host::set_error("fat_paged_decode: the %s decode kernel takes fp16/bf16 queries, head_dim 64 or 128, "
+                        "power-of-two pages of at least %d rows and non-negative K/V strides with pages below "
+                        "4 GB (page_size %d, head_dim %d); use FAT_KERNEL_AUTO or FAT_KERNEL_DECODE_GENERIC",
+                        a->kernel == FAT_KERNEL_DECODE_VALU ? "VALU" : "MFMA", rpl, a->page_size, D);
     return FAT_E_UNSUPPORTED;
   }
   if (generic && T > 1) {

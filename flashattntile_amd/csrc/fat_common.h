@@ -29,6 +29,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
+constexpr int kBufFlags = 0x00020000;
 
 // ---------------------------------------------------------------------------
 // Bit casts and 16-bit float pairs packed in one dword.

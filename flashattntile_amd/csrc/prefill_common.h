@@ -42,8 +42,6 @@ constexpr int kWideBM = 512;
 // kWideBM items).
 constexpr int kWideRankMaxSeqs = 16;
 constexpr int kBN = 64;
-// Dword 3 of a raw (stride 0, offset-enabled) gfx950 buffer descriptor.
-constexpr int kBufFlags = 0x00020000;
 
 // Lazy-rescale bound of the ping-pong kernel (log2 units) and the partial
 // row-sum level above which its exact softmax path runs.
