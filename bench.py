@@ -264,6 +264,7 @@ def _auto_waves(kernel, batch, group, hkv, split, pps, max_pages, page):
 
 def bench_decode(args, device):
     from flashattntile_amd import _hip
+    from flashattntile_amd.kernels.decode import merge_counters
     from flashattntile_amd.autotune import bytes_decode_paged
 
     B, CTX, HQ, HKV, D, P = 32, 4096, 32, 8, 128, 16
@@ -282,11 +283,12 @@ def bench_decode(args, device):
 
     def make(split, waves, kernel):
         pps = auto_chunk if split == auto_split else 0
+        cnt = merge_counters(q, split)  # split-K: the product's merge inside the decode launch
 
         def step(i):
             k, v, _, _ = pools[i % len(pools)]
             _hip.paged_decode(q, k, v, table, lens, out, P, scale, split, workspace=ws, stream=handle,
-                              waves_per_group=waves, pages_per_split=pps, kernel=kernel)
+                              waves_per_group=waves, pages_per_split=pps, kernel=kernel, counters=cnt)
         return step
 
     if args.tune:
@@ -521,6 +523,7 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
+    from flashattntile_amd.kernels.decode import merge_counters
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
@@ -538,13 +541,15 @@ def _decode_row(name, lens, hq, hkv, d, page, device, args, flush, split=None, q
         sk, pps, waves, kern, source = _product_launch(q, pools, table, seq, page, max(lens), total_pages)
     out = torch.empty_like(q)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens), hq, d, sk)), dtype=torch.uint8, device=device)
+    cnt = merge_counters(q, sk)  # the product's split-K merge inside the decode launch
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
 
     def step(i):
         k, v, ks, vs = pools[i % copies]
         _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
-                          k_scale=ks, v_scale=vs, pages_per_split=pps, waves_per_group=waves, kernel=kern)
+                          k_scale=ks, v_scale=vs, pages_per_split=pps, waves_per_group=waves, kernel=kern,
+                          counters=cnt)
 
     steps = max(20, args.steps // 4)
     if pool_bytes * copies < 2 * MALL_BYTES:
@@ -591,6 +596,7 @@ def _configs0_row(device, args, flush):
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
+    from flashattntile_amd.kernels.decode import merge_counters
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged
 
@@ -606,12 +612,13 @@ def _configs0_row(device, args, flush):
     sk, pps, waves, kern, source = _product_launch(qd, pools, td, ld, 16, int(lens.max()), 256)
     out = torch.empty_like(qd)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(4, 32, 128, sk)), dtype=torch.uint8, device=device)
+    cnt = merge_counters(qd, sk)
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
 
     def step(i):
         _hip.paged_decode(qd, kd, vd, td, ld, out, 16, 128 ** -0.5, sk, workspace=ws, stream=handle,
-                          pages_per_split=pps, waves_per_group=waves, kernel=kern)
+                          pages_per_split=pps, waves_per_group=waves, kernel=kern, counters=cnt)
 
     ms = _time_steps_flushed(step, max(20, args.steps // 4), 5, stream, flush)
     nbytes = bytes_decode_paged(lens.tolist(), 32, 8, 128)
@@ -721,6 +728,7 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import _hip
+    from flashattntile_amd.kernels.decode import merge_counters
     from flashattntile_amd.autotune import bytes_decode_paged
     from oracle.reference import ref_attention_paged_prefill
 
@@ -733,13 +741,14 @@ def _multi_decode_row(name, lens, T, device, args, hq=32, hkv=8, d=128, page=16)
     sk, pps, waves, kern, source = _product_launch(q, pools, table, seq, page, max(lens), total_pages, q_len=T)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(len(lens) * T, hq, d, sk)), dtype=torch.uint8,
                      device=device)
+    cnt = merge_counters(q, sk)
     stream = torch.cuda.current_stream(device)
     handle = int(stream.cuda_stream)
 
     def step(i):
         k, v, _, _ = pools[i % 2]
         _hip.paged_decode(q, k, v, table, seq, out, page, d ** -0.5, sk, workspace=ws, stream=handle,
-                          pages_per_split=pps, waves_per_group=waves, kernel=kern)
+                          pages_per_split=pps, waves_per_group=waves, kernel=kern, counters=cnt)
 
     ms = _time_steps(step, max(20, args.steps // 4), 5, stream)
     nbytes = bytes_decode_paged(lens, hq, hkv, d) + 2 * len(lens) * (T - 1) * hq * d * 2
@@ -771,7 +780,7 @@ def _graph_decode_row(name, B, ctx, device, args, hq=32, hkv=8, d=128, page=16, 
     if args.only and args.only not in name:
         return None
     from flashattntile_amd import PagedKVCache, _hip
-    from flashattntile_amd.kernels.decode import paged_decode_launch
+    from flashattntile_amd.kernels.decode import merge_counters, paged_decode_launch
 
     q, pools, table, seq, _, _ = _paged_inputs([ctx] * B, hq, hkv, d, page, torch.float16, seed=17, device=device,
                                                copies=1)
@@ -781,10 +790,11 @@ def _graph_decode_row(name, B, ctx, device, args, hq=32, hkv=8, d=128, page=16, 
     kname = {0: None, 1: "valu", 2: "mfma"}[kern]
     out = torch.empty_like(q)
     ws = torch.empty(max(1, _hip.decode_workspace_bytes(B, hq, d, sk)), dtype=torch.uint8, device=device)
+    cnt = merge_counters(q, sk)
 
     def launch():
         paged_decode_launch(q, cache, d ** -0.5, sk, out=out, workspace=ws, waves_per_group=waves,
-                            pages_per_split=pps, kernel=kname)
+                            pages_per_split=pps, kernel=kname, counters=cnt)
 
     def step():
         for _ in range(layers):

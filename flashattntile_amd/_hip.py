@@ -20,7 +20,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfat_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # enum fat_dtype
 DT_F16 = 0
@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "fat_abi_version",
     "fat_last_error",
     "fat_paged_decode_workspace_bytes",
+    "fat_paged_decode_counters_bytes",
     "fat_paged_decode",
     "fat_paged_decode_noalloc",
     "fat_prefill_workspace_bytes",
@@ -109,6 +110,7 @@ class DecodeArgs(ctypes.Structure):
         ("out_stride_t", _c_i64),
         ("q_len", _c_i32),
         ("kernel", _c_i32),
+        ("merge_counters", _c_vp),
     ]
 
 
@@ -394,6 +396,11 @@ def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, split_k: i
     return int(lib().fat_paged_decode_workspace_bytes(batch, num_heads, head_dim, split_k))
 
 
+def decode_counters_bytes(rows: int, num_heads: int) -> int:
+    """Bytes of the split-K merge counters for ``rows`` = batch * q_len."""
+    return int(lib().fat_paged_decode_counters_bytes(rows, num_heads))
+
+
 def prefill_workspace_bytes(total_k: int, num_kv_heads: int, head_dim: int) -> int:
     return int(lib().fat_prefill_workspace_bytes(total_k, num_kv_heads, head_dim))
 
@@ -424,14 +431,17 @@ def paged_decode(
     waves_per_group: int = 0,
     pages_per_split: int = 0,
     kernel: int = KERNEL_AUTO,
+    counters: torch.Tensor | None = None,
 ) -> None:
     """Enqueue ``fat_paged_decode`` for already-validated device tensors.
 
     ``q``/``out`` are ``[B, H, D]`` (one query per sequence) or
-    ``[B, T, H, D]`` (multi-token decode, ``q_len = T``)."""
+    ``[B, T, H, D]`` (multi-token decode, ``q_len = T``).  ``counters``:
+    zeroed int32 merge counters (``decode_counters_bytes``) for the split-K
+    merge inside the decode launch, or None (a second kernel merges)."""
     a = decode_args(q, k_cache, v_cache, page_table, seq_lens, out, page_size, softmax_scale, split_k,
                     workspace=workspace, k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group,
-                    pages_per_split=pages_per_split, kernel=kernel)
+                    pages_per_split=pages_per_split, kernel=kernel, counters=counters)
     handle = current_stream_handle(q.device) if stream is None else stream
     _check(lib().fat_paged_decode(ctypes.byref(a), _c_vp(handle)), "fat_paged_decode")
 
@@ -452,6 +462,7 @@ def decode_args(
     waves_per_group: int = 0,
     pages_per_split: int = 0,
     kernel: int = KERNEL_AUTO,
+    counters: torch.Tensor | None = None,
 ) -> DecodeArgs:
     """The ``fat_decode_args`` block of a decode launch (see paged_decode)."""
     multi = q.dim() == 4
@@ -491,6 +502,7 @@ def decode_args(
     a.pages_per_split = int(pages_per_split)
     a.softmax_scale = float(softmax_scale)
     a.kernel = int(kernel)
+    a.merge_counters = _ptr(counters)
     return a
 
 

@@ -35,6 +35,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -177,6 +178,166 @@ __device__ __forceinline__ int first_page_ids(int* pid, const int32_t* ptrow, co
 #pragma unroll
   for (int i = 0; i < N; ++i) asm("" : "+s"(pid[i]), "+s"(seq_len));
   return seq_len;
+}
+
+// One output element of the split-K merge: row bh (its S partitions'
+// (acc, m, l) in the workspace), head dim d, stored at element o of out.
+// SMAX (a power of two >= S) fixes the trip count so the loops unroll:
+// every partition's (m, l) and acc loads are issued before the first is used,
+// one memory latency instead of one per partition.  Padded partitions
+// (s >= S) re-read partition S - 1, so every address is inside the row, and
+// are then given m = -inf (weight 0).
+// COH: the rows were written by other workgroups of this launch with
+// device-scope stores (ws_store); they are read with device-scope loads.
+template <bool COH>
+__device__ __forceinline__ float ws_load(const float* ptr) {
+  if constexpr (COH) return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *ptr;
+}
+__device__ __forceinline__ void ws_store(float* ptr, float v, bool coh) {
+  if (coh) __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *ptr = v;
+}
+
+template <typename QT, int SMAX, bool COH = false>
+__device__ __forceinline__ void merge_elem(const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+                                           int64_t bh, int d, int D, int S, uint8_t* out, int64_t o) {
+  const float* ml = ws_ml + bh * S * 2;
+  const float* acc = ws_acc + bh * S * D + d;
+  float m[SMAX], l[SMAX], a[SMAX];
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    const int sc = min(s, S - 1);
+    m[s] = ws_load<COH>(ml + 2 * sc);
+    l[s] = ws_load<COH>(ml + 2 * sc + 1);
+    a[s] = ws_load<COH>(acc + (int64_t)sc * D);
+  }
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) {
+    if (s >= S) {
+      m[s] = -INFINITY;
+      l[s] = 0.f;
+      a[s] = 0.f;
+    }
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < SMAX; ++s) M = fmaxf(M, m[s]);
+  float A = 0.f, L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const float f = fast_exp2(m[s] - M);  // 0 for padded or empty partitions
+      A = __builtin_fmaf(a[s], f, A);
+      L = __builtin_fmaf(l[s], f, L);
+    }
+  }
+  store_elem<QT>(out, o, L > 0.f ? A / L : 0.f);
+}
+
+// The merge of merge_in_launch, with merge_elem's arithmetic: per row j (one
+// thread each) M = max_s m_s, the weights f_s = 2^(m_s - M) (0 for padded
+// partitions) and L = sum_s l_s f_s in partition order, kept in LDS; per
+// output element A = sum_s acc_s f_s in partition order and A / L.  A
+// thread takes at most two elements (the host fuses the merge only then)
+// and issues their partial sums' loads together with its row's (m, l), so
+// the merge waits for one memory latency.
+template <typename QT, int D, int SMAX, typename RowOf>
+__device__ __forceinline__ void merge_rows(const DecodeParams& p, int S, int nrows, RowOf row_of, float* s_f,
+                                           float* s_l) {
+  const int n = nrows * D;
+  const int e0 = threadIdx.x, e1 = threadIdx.x + blockDim.x;  // this thread's elements (if < n)
+  float a0[SMAX], a1[SMAX];
+  int64_t o0 = 0, o1 = 0;
+  auto load_acc = [&](int e, float (&a)[SMAX], int64_t& o) {
+    const int j = e / D;
+    const int d = e - j * D;
+    int64_t bh;
+    row_of(j, bh, o);
+    o += d;
+    const float* acc = p.ws_acc + bh * S * D + d;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) a[s] = s < S ? ws_load<true>(acc + (int64_t)s * D) : 0.f;
+  };
+  if (e0 < n) load_acc(e0, a0, o0);
+  if (e1 < n) load_acc(e1, a1, o1);
+  if (threadIdx.x < nrows) {
+    const int j = threadIdx.x;
+    int64_t bh, o;
+    row_of(j, bh, o);
+    const float* ml = p.ws_ml + bh * S * 2;
+    float m[SMAX], l[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const int sc = min(s, S - 1);
+      m[s] = ws_load<true>(ml + 2 * sc);
+      l[s] = ws_load<true>(ml + 2 * sc + 1);
+    }
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s >= S) {
+        m[s] = -INFINITY;
+        l[s] = 0.f;
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) M = fmaxf(M, m[s]);
+    float L = 0.f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      const float f = M != -INFINITY ? fast_exp2(m[s] - M) : 0.f;
+      s_f[j * SMAX + s] = f;
+      L = __builtin_fmaf(l[s], f, L);
+    }
+    s_l[j] = M != -INFINITY ? L : -1.f;  // -1: no partition saw a key (output 0, as merge_elem)
+  }
+  __syncthreads();
+  auto finish = [&](int e, const float (&a)[SMAX], int64_t o) {
+    const int j = e / D;
+    const float L = s_l[j];
+    float A = 0.f;
+    if (L >= 0.f) {
+#pragma unroll
+      for (int s = 0; s < SMAX; ++s) A = __builtin_fmaf(a[s], s_f[j * SMAX + s], A);
+    }
+    store_elem<QT>(p.out, o, L > 0.f ? A / L : 0.f);
+  };
+  if (e0 < n) finish(e0, a0, o0);
+  if (e1 < n) finish(e1, a1, o1);
+}
+
+// Split-K merge inside the decode launch (p.counters set).  Every thread has
+// written its part of this workgroup's (acc, m, l) rows with device-scope
+// stores (ws_store: written through to the level all XCDs share, no L2
+// write-back needed); each wave waits for its stores to complete, then the
+// workgroup counts itself in on its (sequence, head group) counter with a
+// device-scope atomic.  The one that brings it to S reads all S partitions
+// of the group's rows j < nrows (row_of(j) -> workspace row bh and the
+// output row's first element) with device-scope loads, merges them and puts
+// the counter back to zero for the next launch.  No workgroup waits for
+// another, and no cache is written back or invalidated as a whole.
+template <typename QT, int D, typename RowOf>
+__device__ __forceinline__ void merge_in_launch(const DecodeParams& p, int S, int nrows, RowOf row_of) {
+  __shared__ int s_last;
+  __shared__ float s_f[32 * 16];  // merge weights of up to 32 rows x 16 partitions
+  __shared__ float s_l[32];
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the row stores before the wait
+  __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0): this wave's row stores are complete
+  __syncthreads();
+  int* const cnt = p.counters + (blockIdx.z * gridDim.y + blockIdx.y);
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == S - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  switch (p.smax) {
+    case 4: merge_rows<QT, D, 4>(p, S, nrows, row_of, s_f, s_l); break;
+    case 8: merge_rows<QT, D, 8>(p, S, nrows, row_of, s_f, s_l); break;
+    default: merge_rows<QT, D, 16>(p, S, nrows, row_of, s_f, s_l); break;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename QT, int KV, int D, int HG, int NW>
@@ -508,12 +669,20 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
       *op = Pair<QT>::from_float(o);
     } else {
       const int64_t row = ((int64_t)b * p.H + h) * S + split;
-      p.ws_acc[row * D + d] = A;
+      const bool coh = p.counters != nullptr;
+      ws_store(p.ws_acc + row * D + d, A, coh);
       if (d == 0) {
-        p.ws_ml[row * 2 + 0] = M;
-        p.ws_ml[row * 2 + 1] = L;
+        ws_store(p.ws_ml + row * 2 + 0, M, coh);
+        ws_store(p.ws_ml + row * 2 + 1, L, coh);
       }
     }
+  }
+  if (S > 1 && p.counters) {
+    merge_in_launch<QT, D>(p, S, nvalid, [&](int j, int64_t& bh, int64_t& o) {
+      const int h = head0 + j;
+      bh = (int64_t)b * p.H + h;
+      o = (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
+    });
   }
 }
 
@@ -844,22 +1013,30 @@ void paged_decode_mfma_kernel(const DecodeParams p) {
       *op = Pair<QT>::from_float(L > 0.f ? A / L : 0.f);
     } else {
       const int64_t row = (((int64_t)b * p.T + tt) * p.H + h) * S + split;
-      p.ws_acc[row * D + d] = A;
+      const bool coh = p.counters != nullptr;
+      ws_store(p.ws_acc + row * D + d, A, coh);
       if (d == 0) {
-        p.ws_ml[row * 2 + 0] = M;
-        p.ws_ml[row * 2 + 1] = L;
+        ws_store(p.ws_ml + row * 2 + 0, M, coh);
+        ws_store(p.ws_ml + row * 2 + 1, L, coh);
       }
     }
+  }
+  if (S > 1 && p.counters) {
+    merge_in_launch<QT, D>(p, S, nvalid, [&](int j, int64_t& bh, int64_t& o) {
+      const int rr = row_base + j;
+      const int tt = rr / p.group;
+      const int h = kvh * p.group + (rr - tt * p.group);
+      bh = ((int64_t)b * p.T + tt) * p.H + h;
+      o = (int64_t)b * p.o_sb + (int64_t)tt * p.o_st + (int64_t)h * p.o_sh;
+    });
   }
 }
 
 // Log-sum-exp merge of split-K partitions (decode.py:316-356 semantics):
 //   M = max_s m_s, w_s = 2^(m_s - M), o = sum_s acc_s w_s / sum_s l_s w_s.
-// Rows are (sequence, token, head) with T tokens per sequence.  SMAX (a
-// power of two >= S) fixes the trip count so the loops unroll: every
-// partition's (m, l) and acc loads of a thread are issued before the first
-// is used, one memory latency per launch instead of one per partition (a
-// runtime-bounded loop issued them one at a time: 12.9 us at S = 32).
+// Rows are (sequence, token, head) with T tokens per sequence: one launch
+// per decode (decode_merge_kernel), or inside the decode launch by its last
+// partition (merge_in_launch), with the same arithmetic.
 template <typename QT, int SMAX>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ ws_acc,
                                                            const float* __restrict__ ws_ml, uint8_t* out,
@@ -873,39 +1050,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
   const int64_t bt = bh / H;
   const int t = bt % T;
   const int b = bt / T;
-  const float* ml = ws_ml + bh * S * 2;
-  const float* acc = ws_acc + bh * S * D + d;
-  // Padded partitions (s >= S) re-read partition S - 1, so every address is
-  // inside this row, and are then given m = -inf (weight 0).
-  float m[SMAX], l[SMAX], a[SMAX];
-#pragma unroll
-  for (int s = 0; s < SMAX; ++s) {
-    const int sc = min(s, S - 1);
-    m[s] = ml[2 * sc];
-    l[s] = ml[2 * sc + 1];
-    a[s] = acc[(int64_t)sc * D];
-  }
-#pragma unroll
-  for (int s = 0; s < SMAX; ++s) {
-    if (s >= S) {
-      m[s] = -INFINITY;
-      l[s] = 0.f;
-      a[s] = 0.f;
-    }
-  }
-  float M = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < SMAX; ++s) M = fmaxf(M, m[s]);
-  float A = 0.f, L = 0.f;
-  if (M != -INFINITY) {
-#pragma unroll
-    for (int s = 0; s < SMAX; ++s) {
-      const float f = fast_exp2(m[s] - M);  // 0 for padded or empty partitions
-      A = __builtin_fmaf(a[s], f, A);
-      L = __builtin_fmaf(l[s], f, L);
-    }
-  }
-  store_elem<QT>(out, (int64_t)b * o_sb + (int64_t)t * o_st + (int64_t)h * o_sh + d, L > 0.f ? A / L : 0.f);
+  merge_elem<QT, SMAX>(ws_acc, ws_ml, bh, d, D, S, out, (int64_t)b * o_sb + (int64_t)t * o_st + (int64_t)h * o_sh + d);
 }
 
 }  // namespace fat
@@ -1014,6 +1159,13 @@ extern "C" size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_he
   return (size_t)batch * num_heads * split_k * (head_dim + 2) * sizeof(float);
 }
 
+// One counter per (query row, head): at least one per (sequence, token
+// group, head group) of any kernel's grid.
+extern "C" size_t fat_paged_decode_counters_bytes(int32_t rows, int32_t num_heads) {
+  if (rows <= 0 || num_heads <= 0) return 0;
+  return (size_t)rows * num_heads * sizeof(int32_t);
+}
+
 extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   fat_host::clear_error();
   if (!a) {
@@ -1073,6 +1225,10 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   }
   if (a->split_k > 1 && !a->workspace) {
     fat_host::set_error("fat_paged_decode: split_k > 1 needs a workspace");
+    return FAT_E_INVALID;
+  }
+  if ((uintptr_t)a->merge_counters & 3) {
+    fat_host::set_error("fat_paged_decode: merge_counters must be 4-byte aligned");
     return FAT_E_INVALID;
   }
   if (a->q_len < 0 || a->q_len > 64) {
@@ -1185,6 +1341,20 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   prm.max_pages = a->max_pages;
   prm.pps_fixed = a->pages_per_split;
   prm.scale_log2 = a->softmax_scale * fat::kLog2e;
+  // Split-K merge inside the decode launch (VALU and MFMA kernels, split_k
+  // <= 16) when the caller gives the counters and a workgroup's rows make at
+  // most two output elements per thread: the last workgroup of a head group
+  // merges alone, so wider groups (e.g. MQA's 32 heads) and more partitions
+  // keep the merge kernel, which spreads the elements over many workgroups
+  // (measured on MI355X: 32 partitions merged in the launch ran 1-11 %
+  // slower, 16 and fewer 2-21 % faster).
+  const int S = a->split_k;
+  auto use_fused = [&](int rows_per_wg, int nw) {
+    return S > 1 && S <= 16 && a->merge_counters != nullptr && rows_per_wg * D <= 2 * 64 * nw;
+  };
+  bool fused = false;
+  prm.counters = nullptr;
+  prm.smax = S <= 4 ? 4 : S <= 8 ? 8 : 16;
 
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const dim3 grid(a->split_k, a->num_kv_heads * hg_per_kv, a->batch);
@@ -1202,10 +1372,12 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
     // MI355X); short partitions finish sooner with 4.
     int nw = a->waves_per_group ? a->waves_per_group
                                 : ((wgs < 2 * 256 && pages_per_wg * a->page_size >= 2048) ? 8 : 4);
+    fused = use_fused(std::min(32, group * T), nw);
+    prm.counters = fused ? a->merge_counters : nullptr;
     if (a->q_dtype == FAT_DTYPE_F16) launch_decode_mfma_q<fat::F16>(prm, kv, D, nw, grid, stream);
     else launch_decode_mfma_q<fat::BF16>(prm, kv, D, nw, grid, stream);
     const int rc = fat_host::launch_status("paged_decode_mfma_kernel");
-    if (rc != FAT_OK || a->split_k == 1) return rc;
+    if (rc != FAT_OK || a->split_k == 1 || fused) return rc;
     return launch_merge(prm, a, D, stream);
   }
   // 8-wave workgroups keep more loads in flight per CU.  They pay off when
@@ -1215,9 +1387,11 @@ extern "C" int fat_paged_decode(const fat_decode_args* a, void* stream_ptr) {
   // finish sooner with 4.
   const int nw = a->waves_per_group ? a->waves_per_group
                                     : ((wgs < 2 * 256 || pages_per_wg * a->page_size >= 1024) ? 8 : 4);
+  fused = use_fused(std::min(HG, group), nw);
+  prm.counters = fused ? a->merge_counters : nullptr;
   int rc = (a->q_dtype == FAT_DTYPE_F16) ? launch_decode_q<fat::F16>(prm, kv, D, HG, nw, grid, stream)
                                          : launch_decode_q<fat::BF16>(prm, kv, D, HG, nw, grid, stream);
-  if (rc != FAT_OK || a->split_k == 1) return rc;
+  if (rc != FAT_OK || a->split_k == 1 || fused) return rc;
 
   return launch_merge(prm, a, D, stream);
 }
@@ -1290,6 +1464,7 @@ extern "C" int fat_paged_decode_noalloc(const fat_decode_args* a, void* stream) 
   }
   fat_decode_args b = *a;
   b.workspace = need ? g_scratch_ptr[dev] : nullptr;
+  b.merge_counters = nullptr;  // a second kernel merges: no state outside the scratch array
   const int rc = fat_paged_decode(&b, stream);
   if (rc != FAT_OK) {
     // Name this entry in the message the shared path set.

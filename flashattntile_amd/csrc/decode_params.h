@@ -33,6 +33,12 @@ struct DecodeParams {
   int32_t P, log2P, num_pages, max_pages;  // log2P = -1: page_size not a power of two
   int32_t pps_fixed;  // pages per partition, 0 = ceil(np / split_k)
   float scale_log2;  // softmax_scale * log2(e)
+  // Split-K merge inside the decode launch: one counter per (sequence, head
+  // group) = blockIdx.z * gridDim.y + blockIdx.y, zero between launches;
+  // nullptr: a second kernel merges.  smax: the merge's unrolled partition
+  // count (a power of two >= split_k, at most 16).
+  int32_t* counters;
+  int32_t smax;
 };
 
 }  // namespace fat

@@ -199,6 +199,30 @@ def _require_rocm(q: torch.Tensor, cache: PagedKVCache, what: str) -> None:
         )
 
 
+# Split-K merge counters of the one-call decode paths: one zeroed int32
+# buffer per (device, stream), grown on demand.  Every launch leaves its
+# counters zero, so launches in one stream's order share them; launches on
+# other streams get their own.
+_MERGE_COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def merge_counters(q: torch.Tensor, split_k: int) -> torch.Tensor | None:
+    """Zeroed merge counters for a split-K launch of ``q`` on torch's current
+    stream (None when ``split_k`` is 1): the decode kernels then merge the
+    partitions themselves instead of a second kernel."""
+    if split_k <= 1:
+        return None
+    rows = q.shape[0] * (q.shape[1] if q.dim() == 4 else 1)
+    n = _hip.decode_counters_bytes(rows, q.shape[-2]) // 4
+    key = (q.device.index if q.device.index is not None else torch.cuda.current_device(),
+           _hip.current_stream_handle(q.device))
+    t = _MERGE_COUNTERS.get(key)
+    if t is None or t.numel() < n:
+        t = torch.zeros(max(n, 4096), dtype=torch.int32, device=q.device)
+        _MERGE_COUNTERS[key] = t
+    return t
+
+
 def paged_decode_launch(
     q: torch.Tensor,
     cache: PagedKVCache,
@@ -210,6 +234,7 @@ def paged_decode_launch(
     waves_per_group: int | None = None,
     pages_per_split: int = 0,
     kernel: str | None = None,
+    counters: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Enqueue the HIP decode without validation or synchronisation.
 
@@ -217,7 +242,10 @@ def paged_decode_launch(
     contiguous fp16/bf16 on the cache's device; ``out`` (default
     ``empty_like(q)``) and ``workspace`` (default: allocated) may be passed in
     to avoid allocations.  ``kernel``: None (library's choice), ``"valu"`` or
-    ``"mfma"``.
+    ``"mfma"``.  ``counters``: zeroed int32 split-K merge counters
+    (:func:`merge_counters`, or any buffer of ``decode_counters_bytes`` that
+    only this stream's launches use); the decode launch then merges its
+    partitions itself.  None: a second kernel merges.
     """
     if cache.k_cache.stride(-1) != 1 or cache.v_cache.stride(-1) != 1:
         raise ValueError("k_cache and v_cache need a contiguous head_dim axis")
@@ -235,10 +263,13 @@ def paged_decode_launch(
     if scales is not None:
         k_scale = scales["k"] if isinstance(scales, dict) else scales.k
         v_scale = scales["v"] if isinstance(scales, dict) else scales.v
+    if counters is not None and counters.numel() * counters.element_size() < _hip.decode_counters_bytes(
+            rows, q.shape[-2]):
+        raise ValueError("paged_decode_launch: counters smaller than decode_counters_bytes(rows, num_heads)")
     _hip.paged_decode(q, cache.k_cache, cache.v_cache, pt, sl, out,
                       cache.page_size, softmax_scale, split_k, workspace=workspace,
                       k_scale=k_scale, v_scale=v_scale, waves_per_group=waves_per_group or 0,
-                      pages_per_split=pages_per_split, kernel=_KERNEL_CODES[kernel])
+                      pages_per_split=pages_per_split, kernel=_KERNEL_CODES[kernel], counters=counters)
     return out
 
 
@@ -269,8 +300,10 @@ def paged_decode_attention(
         raise ValueError(f"paged_decode_attention: dtype {q.dtype} is not fp16/bf16/fp32 (the HIP kernels' types)")
     if cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
-    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"],
-                               pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"])
+    q = q.contiguous()
+    return paged_decode_launch(q, cache, scale, cfg["split_k"], waves_per_group=cfg["num_warps"],
+                               pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"],
+                               counters=merge_counters(q, cfg["split_k"]))
 
 
 def paged_decode_attention_fp8(
@@ -304,10 +337,11 @@ def paged_decode_attention_fp8(
         raise ValueError(f"quantised decode requires fp16/bf16 queries, got {q.dtype}")
     if k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32:
         raise ValueError("scales must be float32")
-    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"],
+    q = q.contiguous()
+    return paged_decode_launch(q, cache, scale, cfg["split_k"],
                                scales={"k": k_scale.contiguous(), "v": v_scale.contiguous()},
                                waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"],
-                               kernel=cfg["kernel"])
+                               kernel=cfg["kernel"], counters=merge_counters(q, cfg["split_k"]))
 
 
 def paged_decode_attention_multi(
@@ -351,9 +385,10 @@ def paged_decode_attention_multi(
         sc = {"k": k_scale.contiguous(), "v": v_scale.contiguous()}
     elif cache.k_cache.dtype != q.dtype:
         raise ValueError(f"q dtype {q.dtype} must match cache dtype {cache.k_cache.dtype}")
-    return paged_decode_launch(q.contiguous(), cache, scale, cfg["split_k"], scales=sc,
+    q = q.contiguous()
+    return paged_decode_launch(q, cache, scale, cfg["split_k"], scales=sc,
                                waves_per_group=cfg["num_warps"], pages_per_split=cfg["pages_per_split"],
-                               kernel=cfg["kernel"])
+                               kernel=cfg["kernel"], counters=merge_counters(q, cfg["split_k"]))
 
 
 class DecodeLaunch:
@@ -413,6 +448,11 @@ class DecodeLaunch:
         rows = q.shape[0] * q_len
         need = _hip.decode_workspace_bytes(rows, q.shape[-2], q.shape[-1], cfg["split_k"])
         self.workspace = torch.empty(max(1, need), dtype=torch.uint8, device=q.device) if need else None
+        # Zeroed split-K merge counters of this launch (each run leaves them
+        # zero): the decode kernel merges its partitions itself.  Runs of one
+        # DecodeLaunch share them, as they share the workspace.
+        self.counters = (torch.zeros(_hip.decode_counters_bytes(rows, q.shape[-2]) // 4, dtype=torch.int32,
+                                     device=q.device) if cfg["split_k"] > 1 else None)
         self._keep = (cache, k_scale, v_scale)  # the argument block points into these
         self._shape, self._dtype = tuple(q.shape), q.dtype
         self._device = q.device
@@ -420,7 +460,8 @@ class DecodeLaunch:
                                       cache.page_size, self.softmax_scale, cfg["split_k"],
                                       workspace=self.workspace, k_scale=k_scale, v_scale=v_scale,
                                       waves_per_group=cfg["num_warps"] or 0,
-                                      pages_per_split=cfg["pages_per_split"], kernel=_KERNEL_CODES[cfg["kernel"]])
+                                      pages_per_split=cfg["pages_per_split"], kernel=_KERNEL_CODES[cfg["kernel"]],
+                                      counters=self.counters)
 
     def run(self, q: torch.Tensor, out: torch.Tensor | None = None, stream: int | None = None) -> torch.Tensor:
         """Decode ``q`` into ``out`` (default: a new tensor) on ``stream``

@@ -38,7 +38,7 @@ from . import _hip
 from .autotune import (TUNED_CONFIGS_PATH, autotune, build_config_space, bytes_decode_paged, decode_partition,
                        decode_signature, flops_attention, initialize_store, prefill_paged_signature,
                        prefill_signature, save_best, time_back_to_back)
-from .kernels.decode import paged_decode_launch
+from .kernels.decode import merge_counters, paged_decode_launch
 from .kernels.prefill import paged_prefill_launch, prefill_launch
 from .paging import PagedKVCache
 from .quant import quantize_cache
@@ -132,7 +132,8 @@ def tune_decode(device, out_path, min_gain: float) -> None:
             i = turn[0] = (turn[0] + 1) % len(caches)
             paged_decode_launch(q, caches[i], d ** -0.5, cfg["split_k"], out=out, workspace=ws,
                                 scales=scale_list[i], waves_per_group=cfg["num_warps"],
-                                pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"])
+                                pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"],
+                                counters=merge_counters(q, cfg["split_k"]))
 
         nbytes = bytes_decode_paged([ctx] * batch, hq * q_len, hkv, d, kv_elem_bytes=1 if quantized else 2,
                                     page_size=P, quantized=quantized)

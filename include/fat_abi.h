@@ -46,7 +46,9 @@
 extern "C" {
 #endif
 
-/* 13: fat_cache_stats (paged-cache validation in one launch).
+/* 14: fat_decode_args.merge_counters and fat_paged_decode_counters_bytes:
+ *     split-K decode merges its partitions inside the decode launch.
+ * 13: fat_cache_stats (paged-cache validation in one launch).
  * 12: fat_prefill_paged_args.workspace and
  *     fat_prefill_paged_workspace_bytes: long paged prefill chunks run on
  *     the wide kernel through packed copies of their K/V rows.
@@ -61,7 +63,7 @@ extern "C" {
  * 8: fp32 decode, any page size and head_dim 32/256 through the generic
  *    decode kernel (FAT_KERNEL_DECODE_GENERIC); the paged prefill `rows`
  *    field replaces the library's environment overrides. */
-#define FAT_ABI_VERSION 13
+#define FAT_ABI_VERSION 14
 
 /* Element types understood by the kernels. */
 enum fat_dtype {
@@ -193,6 +195,18 @@ typedef struct fat_decode_args {
   int64_t q_stride_t, out_stride_t;
   int32_t q_len;
   int32_t kernel; /* FAT_KERNEL_AUTO, _DECODE_VALU, _MFMA or _GENERIC */
+  /* Optional (split_k > 1): int32 counters, one per (sequence, query head),
+   * fat_paged_decode_counters_bytes(batch * q_len, num_heads) bytes, all
+   * zero before the first launch that uses them; every launch leaves them
+   * zero.  With them the VALU and MFMA kernels merge the partitions in the
+   * decode launch itself (the last partition of each head group to finish
+   * merges them, with the arithmetic of the merge kernel: bit-identical
+   * results) when split_k <= 16 and a workgroup's heads make at most two
+   * output elements per thread (the last workgroup merges alone); otherwise
+   * (NULL, more partitions or heads, the generic kernel) a second kernel
+   * merges and the counters are not touched.  Launches that may run at the
+   * same time (other streams) must not share counters. */
+  int32_t* merge_counters;
 } fat_decode_args;
 
 /*
@@ -385,6 +399,10 @@ const char* fat_last_error(void);
 size_t fat_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads,
                                         int32_t head_dim, int32_t split_k);
 
+/* Bytes of fat_decode_args.merge_counters for `rows` = batch * q_len query
+ * rows (q_len 1 for single-query decode) of num_heads heads. */
+size_t fat_paged_decode_counters_bytes(int32_t rows, int32_t num_heads);
+
 /* Enqueue paged decode (fp16/bf16/fp32/int8/fp8 K/V) on `stream`.
  * Replaces flashattn_tile/kernels/decode.py:533-704 (see file header). */
 int fat_paged_decode(const fat_decode_args* args, void* stream);
@@ -394,7 +412,8 @@ int fat_paged_decode(const fat_decode_args* args, void* stream);
  * serving loops and harnesses that forbid hipMalloc).  The same launch as
  * fat_paged_decode(args, stream), except that the split-K workspace is a
  * device array inside the library (FAT_DECODE_NOALLOC_MAX_WORKSPACE bytes
- * per GPU, held until the process ends); args->workspace is ignored.  The
+ * per GPU, held until the process ends); args->workspace and
+ * args->merge_counters are ignored (a second kernel merges).  The
  * library allocates and frees nothing.  A launch whose workspace
  * (fat_paged_decode_workspace_bytes of its batch * q_len rows) exceeds the
  * maximum returns FAT_E_INVALID.  Every call on one GPU shares that GPU's
