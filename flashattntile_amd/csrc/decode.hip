@@ -309,14 +309,18 @@ __device__ __forceinline__ void merge_rows(const DecodeParams& p, int S, int nro
 
 // Split-K merge inside the decode launch (p.counters set).  Every thread has
 // written its part of this workgroup's (acc, m, l) rows with device-scope
-// stores (ws_store: written through to the level all XCDs share, no L2
-// write-back needed); each wave waits for its stores to complete, then the
-// workgroup counts itself in on its (sequence, head group) counter with a
-// device-scope atomic.  The one that brings it to S reads all S partitions
-// of the group's rows j < nrows (row_of(j) -> workspace row bh and the
-// output row's first element) with device-scope loads, merges them and puts
-// the counter back to zero for the next launch.  No workgroup waits for
-// another, and no cache is written back or invalidated as a whole.
+// stores (ws_store, global_store ... sc1: written through to the level all
+// XCDs share); each wave waits until its stores have completed there
+// (vmcnt(0)), then the workgroup counts itself in on its (sequence, head
+// group) counter with a device-scope atomic.  The workgroup that brings the
+// count to S has therefore seen every other partition's count, each issued
+// after that partition's rows were complete at the shared level; it reads
+// them with device-scope loads (global_load ... sc1), merges them and puts
+// the counter back to zero for the next launch.  The ordering rests on
+// those gfx950 completion rules, not on release/acquire operations: an
+// agent-scope release would write back the whole L2 of the XCD
+// (buffer_wbl2), which measured 7-16 % slower on 8-sequence split
+// launches.  No workgroup waits for another.
 template <typename QT, int D, typename RowOf>
 __device__ __forceinline__ void merge_in_launch(const DecodeParams& p, int S, int nrows, RowOf row_of) {
   __shared__ int s_last;
