@@ -264,15 +264,16 @@ constexpr float kLazy = 8.0f;
 #define FAT_PF_SPLIT_LONG 32
 #endif
 
-// POS: softmax_scale > 0, so max_j(s_j * c) = c * max_j(s_j) and the scale
-// is folded into the exponent's fma; otherwise scores are scaled first.
+// The scale c is positive (launch_prefill folds a negative or zero
+// softmax scale into Q), so max_j(s_j * c) = c * max_j(s_j) and the scale is
+// folded into the exponent's fma.
 // NG = 2: two groups of 4 waves take alternate K/V tiles for the same query
 // rows (group g tiles g, g + 2, ...) and merge (m, l, O) through LDS at the
 // end, halving the tile chain of a query block: for grids too small to
 // give every CU more than one workgroup.
 // D = 256 (NG = 1 only) holds O (128 registers) and Q (64) per lane and runs
 // one wave per SIMD with up to 512 registers.
-template <typename T, int D, bool CAUSAL, bool POS, int PG, int NG>
+template <typename T, int D, bool CAUSAL, int PG, int NG>
 __global__ __launch_bounds__(256 * NG)
 __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2, D >= 256 ? 1 : 2)))
 void prefill_kernel(const PrefillParams p) {
@@ -333,7 +334,7 @@ void prefill_kernel(const PrefillParams p) {
   {
     const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + my_row) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = (*reinterpret_cast<const u32x4*>(qp + 32 * ks) & p.q_and) ^ p.q_xor;
   }
   // Retire the Q loads here: otherwise the compiler's wait-count tracking
   // keeps treating qf as in flight inside the tile loop and makes every
@@ -538,13 +539,7 @@ void prefill_kernel(const PrefillParams p) {
     const int n0 = gtile(tile) * kBN;
     const uint16_t* Vb = Vs[grp][buf];
 
-    // ---- scores of tile t: scale (c <= 0 only), mask, row max ----
-    if (!POS) {
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s_cur[jb][r] *= c;
-    }
+    // ---- scores of tile t: mask, row max ----
     const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
     if (need_mask) {  // wave-uniform: only tiles crossing kv_len or the diagonal
       const int lim = CAUSAL ? min(kv_len - 1, my_row + shift) : kv_len - 1;
@@ -562,7 +557,7 @@ void prefill_kernel(const PrefillParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[jb][r]);
     mx = xor32<OpMax>(mx);
-    if (POS) mx *= c;  // exact: rounding is monotonic and c > 0
+    mx *= c;  // exact: rounding is monotonic and c > 0
     // Lazy rescale: m_run moves only when this tile's max exceeds it by kLazy.
     const bool grow = mx > m_run + kLazy;
     if (__any(grow)) {
@@ -583,7 +578,7 @@ void prefill_kernel(const PrefillParams p) {
     // ---- S(t+1) on the MFMA pipe, interleaved with P(t) = 2^(s c - m) ----
     f32x16 s_nxt[2];
     if constexpr (HAS_NEXT) qk(buf ^ 1, s_nxt);
-    const float cm = POS ? c : 1.f;
+    const float cm = c;
     // NG > 1: a row can have seen no key yet (its keys lie in the other
     // group's tiles); m_run is then -inf and every score is -inf, so P = 0.
     const float nm = (NG > 1 && m_run == -INFINITY) ? 0.f : -m_run;
@@ -722,7 +717,7 @@ struct MfmaPhaseOrder {
   }
 };
 
-template <typename T, int D, bool CAUSAL, bool POS, int PG, bool VPRE>
+template <typename T, int D, bool CAUSAL, int PG, bool VPRE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const PrefillParams p) {
   constexpr int KS = D / 16;
@@ -790,7 +785,7 @@ void prefill_pp_kernel(const PrefillParams p) {
     const int qr = my_row;
     const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = (*reinterpret_cast<const u32x4*>(qp + 32 * ks) & p.q_and) ^ p.q_xor;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): retire the Q loads before the loop
 
@@ -925,12 +920,6 @@ void prefill_pp_kernel(const PrefillParams p) {
   // Softmax of S(t) -> P(t) (mask, max, lazy rescale, exponentials).
   auto softmax = [&](int t) {
     const int n0 = t * kBN;
-    if (!POS) {
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[jb][r] *= c;
-    }
     const bool need_mask = (n0 + kBN > kv_len) || (CAUSAL && n0 + kBN - 1 > row0 + shift);
     if (need_mask) {
       const int lim = CAUSAL ? min(kv_len - 1, my_row + shift) : kv_len - 1;
@@ -947,7 +936,7 @@ void prefill_pp_kernel(const PrefillParams p) {
     // first tile or when some lane's partial row sum exceeds 2^kLazyPP --
     // which every p > 2^kLazyPP forces.  P and the fp32 sums hold values up
     // to 2^kLazyPP exactly as well as values up to 1.
-    const float cm = POS ? c : 1.f;
+    const float cm = c;
     // bf16: element (tt, e2) of this lane holds a key staged by wave
     // ((4g + 8(2tt + e2/2)) mod kRowsPerLoad) / (64 / CPR) of group B; its
     // P is computed as 2^(s c - m + o) with o = s_wave - e_acc <= 0, and its
@@ -996,7 +985,7 @@ void prefill_pp_kernel(const PrefillParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[jb][r]);
       mx = xor32<OpMax>(mx);
-      if (POS) mx *= c;
+      mx *= c;
       const bool grow = mx > m_run + kLazyPP;
       if (__any(grow)) {
         const float alpha = grow ? fast_exp2(m_run - mx) : 1.f;
@@ -1195,21 +1184,13 @@ __global__ __launch_bounds__(256) void bf16v_to_f16_kernel(const uint16_t* __res
 namespace {
 
 template <typename T, int D, bool CAUSAL, int PG, int NG>
-void launch_prefill_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
-  if (pos) {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, true, PG, NG>), grid, dim3(256 * NG), 0, stream, prm);
-  } else {
-    hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, false, PG, NG>), grid, dim3(256 * NG), 0, stream, prm);
-  }
+void launch_prefill_c(const fat::PrefillParams& prm, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((fat::prefill_kernel<T, D, CAUSAL, PG, NG>), grid, dim3(256 * NG), 0, stream, prm);
 }
 
 template <typename T, int D, bool CAUSAL, int PG, bool VPRE = false>
-void launch_prefill_pp_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
-  if (pos) {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, true, PG, VPRE>), grid, dim3(512), 0, stream, prm);
-  } else {
-    hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, false, PG, VPRE>), grid, dim3(512), 0, stream, prm);
-  }
+void launch_prefill_pp_c(const fat::PrefillParams& prm, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((fat::prefill_pp_kernel<T, D, CAUSAL, PG, VPRE>), grid, dim3(512), 0, stream, prm);
 }
 
 // Mean query tokens per sequence from which bf16 packed prefill converts V
@@ -1226,31 +1207,30 @@ size_t vpre_bytes_v16(int64_t total_k, int64_t hkv, int64_t d) {
 
 template <typename T, int D, int PG>
 int launch_prefill_t(const fat::PrefillParams& prm, bool causal, PrefillKind kind, dim3 grid, hipStream_t stream) {
-  const bool pos = prm.scale_log2 > 0.f;
   if constexpr (D == 256) {  // the 4-wave kernel only (launch_prefill checked kind)
     (void)kind;
-    if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, pos, grid, stream);
-    else launch_prefill_c<T, D, false, PG, 1>(prm, pos, grid, stream);
+    if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, grid, stream);
+    else launch_prefill_c<T, D, false, PG, 1>(prm, grid, stream);
     return fat_host::launch_status("prefill_kernel");
   } else {
     if (kind == PF_PINGPONG) {
       if constexpr (std::is_same<T, fat::BF16>::value && PG == 0) {
         if (prm.v_head_scale) {
-          if (causal) launch_prefill_pp_c<T, D, true, PG, true>(prm, pos, grid, stream);
-          else launch_prefill_pp_c<T, D, false, PG, true>(prm, pos, grid, stream);
+          if (causal) launch_prefill_pp_c<T, D, true, PG, true>(prm, grid, stream);
+          else launch_prefill_pp_c<T, D, false, PG, true>(prm, grid, stream);
           return fat_host::launch_status("prefill_pp_kernel");
         }
       }
-      if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, pos, grid, stream);
-      else launch_prefill_pp_c<T, D, false, PG>(prm, pos, grid, stream);
+      if (causal) launch_prefill_pp_c<T, D, true, PG>(prm, grid, stream);
+      else launch_prefill_pp_c<T, D, false, PG>(prm, grid, stream);
       return fat_host::launch_status("prefill_pp_kernel");
     }
     if (kind == PF_4WAVE_SPLIT) {
-      if (causal) launch_prefill_c<T, D, true, PG, 2>(prm, pos, grid, stream);
-      else launch_prefill_c<T, D, false, PG, 2>(prm, pos, grid, stream);
+      if (causal) launch_prefill_c<T, D, true, PG, 2>(prm, grid, stream);
+      else launch_prefill_c<T, D, false, PG, 2>(prm, grid, stream);
     } else {
-      if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, pos, grid, stream);
-      else launch_prefill_c<T, D, false, PG, 1>(prm, pos, grid, stream);
+      if (causal) launch_prefill_c<T, D, true, PG, 1>(prm, grid, stream);
+      else launch_prefill_c<T, D, false, PG, 1>(prm, grid, stream);
     }
     return fat_host::launch_status("prefill_kernel");
   }
@@ -1394,7 +1374,19 @@ int launch_prefill(fat::PrefillParams& prm, int max_seqlen_q, int64_t max_seqlen
   }
   const int bm = kind == PF_WIDE ? fat::kWideBM : kind == PF_PINGPONG ? fat::kPBM : fat::kBM;
   prm.nqb = (max_seqlen_q + bm - 1) / bm;
+  // The MFMA kernels take a positive scale: a negative one runs as its
+  // magnitude with Q's signs flipped as Q is loaded (exact in fp16/bf16 and
+  // through the MFMA sums), a zero one with Q zeroed (every logit 0).
+  prm.q_and = ~0u;
+  prm.q_xor = 0u;
   prm.scale_log2 = softmax_scale * fat::kLog2e;
+  if (softmax_scale < 0.f) {
+    prm.q_xor = 0x80008000u;
+    prm.scale_log2 = -prm.scale_log2;
+  } else if (softmax_scale == 0.f) {
+    prm.q_and = 0u;
+    prm.scale_log2 = fat::kLog2e;
+  }
   const int64_t n = (int64_t)prm.nqb * prm.B * prm.H;
   if (n > 0x7fffffff) {
     fat_host::set_error("%s: too many query blocks (%lld)", who, (long long)n);

@@ -17,7 +17,11 @@ struct PrefillParams {
   uint8_t* out;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh;  // element strides (k/v_st: slot stride when paged)
   int32_t B, H, Hkv, group, nqb;
-  float scale_log2;
+  float scale_log2;  // > 0 (or NaN): the kernels fold it into the exponent's fma
+  // Applied to every Q dword as it is loaded, (q & q_and) ^ q_xor: a
+  // negative softmax scale runs as |scale| with Q's signs flipped (exact),
+  // a zero scale with Q zeroed (every logit 0).  Identity: ~0u, 0.
+  uint32_t q_and, q_xor;
   // Paged K/V (PAGED instantiations only).
   const int32_t* pt;    // page table [B, max_pages]
   const int32_t* lens;  // kv_len per sequence

@@ -152,7 +152,7 @@ __device__ __forceinline__ int wide_ranked_item(const PrefillParams& p, int n, i
   return s_len[2 * B];
 }
 
-template <typename T, bool CAUSAL, bool POS>
+template <typename T, bool CAUSAL>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_wide_kernel(const PrefillParams p) {
   constexpr int D = 128;
@@ -268,7 +268,7 @@ void prefill_wide_kernel(const PrefillParams p) {
     const int qr = max(row0 + 32 * rb + li, 0);
     const uint8_t* qp = p.q + 2 * ((int64_t)(q_start + qr) * p.q_st + (int64_t)h * p.q_sh + 8 * g);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks) qf[rb][ks] = (*reinterpret_cast<const u32x4*>(qp + 32 * ks) & p.q_and) ^ p.q_xor;
   }
   if (n_tiles > 0) issue(0, 0);
   // Wait until this wave's loads of every tile before the most recent issue
@@ -327,14 +327,8 @@ void prefill_wide_kernel(const PrefillParams p) {
   // when the max exceeds it by more than kLazyPP (rescaling O and l), and
   // computes P again; S(t) is then recomputed from the K tile, still in LDS,
   // since the fast path lets S die as P is formed.
-  auto prep = [&](int t) __attribute__((always_inline)) {  // scale (non-positive scales) and mask S(t)
+  auto prep = [&](int t) __attribute__((always_inline)) {  // mask S(t)
     const int n0 = t * kWideBN;
-    if (!POS) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[rb][r] *= c;
-    }
     const bool need_mask = (n0 + kWideBN > kv_len) || (CAUSAL && n0 + kWideBN - 1 > row0 + shift);
     if (need_mask) {
       // Element r of this lane holds key n0 + 4 g + (r & 3) + 8 (r >> 2):
@@ -349,7 +343,7 @@ void prefill_wide_kernel(const PrefillParams p) {
       }
     }
   };
-  const float cm = POS ? c : 1.f;
+  const float cm = c;  // positive: a non-positive scale is folded into Q
   auto compute_p = [&](int rb) __attribute__((always_inline)) -> float {
     const float nm = -m_run[rb];
     float lsq[2];
@@ -373,7 +367,7 @@ void prefill_wide_kernel(const PrefillParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[rb][r]);
       mx = xor32<OpMax>(mx);
-      if (POS) mx *= c;
+      mx *= c;
       const bool grow = mx > m_run[rb] + kLazyPP;
       if (__any(grow)) {
         const float alpha = grow ? fast_exp2(m_run[rb] - mx) : 1.f;
@@ -488,19 +482,17 @@ void prefill_wide_kernel(const PrefillParams p) {
 namespace fat_host {
 
 template <typename T, bool CAUSAL>
-static void launch_wide_c(const fat::PrefillParams& prm, bool pos, dim3 grid, hipStream_t stream) {
-  if (pos) hipLaunchKernelGGL((fat::prefill_wide_kernel<T, CAUSAL, true>), grid, dim3(512), 0, stream, prm);
-  else hipLaunchKernelGGL((fat::prefill_wide_kernel<T, CAUSAL, false>), grid, dim3(512), 0, stream, prm);
+static void launch_wide_c(const fat::PrefillParams& prm, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((fat::prefill_wide_kernel<T, CAUSAL>), grid, dim3(512), 0, stream, prm);
 }
 
 int launch_prefill_wide(const fat::PrefillParams& prm, bool bf16, bool causal, dim3 grid, hipStream_t stream) {
-  const bool pos = prm.scale_log2 > 0.f;
   if (bf16) {
-    if (causal) launch_wide_c<fat::BF16, true>(prm, pos, grid, stream);
-    else launch_wide_c<fat::BF16, false>(prm, pos, grid, stream);
+    if (causal) launch_wide_c<fat::BF16, true>(prm, grid, stream);
+    else launch_wide_c<fat::BF16, false>(prm, grid, stream);
   } else {
-    if (causal) launch_wide_c<fat::F16, true>(prm, pos, grid, stream);
-    else launch_wide_c<fat::F16, false>(prm, pos, grid, stream);
+    if (causal) launch_wide_c<fat::F16, true>(prm, grid, stream);
+    else launch_wide_c<fat::F16, false>(prm, grid, stream);
   }
   return launch_status("prefill_wide_kernel");
 }

@@ -12,10 +12,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from _parity import assert_parity, force_prefill_knobs, make_varlen, ulp
-from flashattntile_amd import prefill_attention
-from flashattntile_amd.kernels.prefill import prefill_launch
-from oracle.reference import ref_attention_varlen
+from _parity import assert_parity, force_prefill_knobs, make_paged, make_varlen, ulp
+from flashattntile_amd import PagedKVCache, prefill_attention
+from flashattntile_amd.kernels.prefill import paged_prefill_attention, prefill_launch
+from oracle.reference import ref_attention_paged_prefill, ref_attention_varlen
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -162,6 +162,30 @@ def test_prefill_kv_longer_than_q(dtype, causal, kernel):
     out = prefill_attention(q, k, v, cq, ck, max(lq), max(lk), causal=causal, softmax_scale=0.07)
     torch.cuda.synchronize()
     assert_parity(out, _ref32(q, k, v, cq, ck, causal, scale=0.07), label=label)
+
+
+@pytest.mark.parametrize("scale", [-0.08, 0.0])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_non_positive_scales(dtype, causal, scale, kernel):
+    """The MFMA kernels take a positive scale: a negative one runs as its
+    magnitude with Q's signs flipped as Q is loaded, a zero one with Q zeroed
+    (every logit 0, so each query averages its visible V rows).  Packed and
+    paged (the wide kernel through staged K/V) against the oracle."""
+    label = f"prefill {kernel} {dtype} scale={scale} causal={causal}"
+    print(label, flush=True)
+    lens = [1, 17, 255, 1000, 640]
+    q, k, v, cu = make_varlen(lens, 32, 8, 128, dtype, seed=71, device=DEV)
+    out = prefill_attention(q, k, v, cu, cu, max(lens), max(lens), causal=causal, softmax_scale=scale)
+    torch.cuda.synchronize()
+    assert_parity(out, _ref32(q, k, v, cu, cu, causal, scale=scale), label=label)
+    kc, vc, pt, sl = make_paged(lens, 8, 128, 16, dtype, seed=72, device=DEV)
+    cache = PagedKVCache(kc, vc, pt, sl, 16)
+    out_p = paged_prefill_attention(q, cache, cu, max(lens), causal=causal, softmax_scale=scale)
+    torch.cuda.synchronize()
+    ref_p = ref_attention_paged_prefill(q.cpu(), kc.cpu(), vc.cpu(), pt.cpu(), sl.cpu(), cu.cpu(), causal=causal,
+                                        softmax_scale=scale, return_fp32=True)
+    assert_parity(out_p, ref_p, label=f"paged {label}")
 
 
 def _wide_pack(n, seed):
