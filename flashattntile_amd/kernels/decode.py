@@ -213,7 +213,7 @@ def merge_counters(q: torch.Tensor, split_k: int) -> torch.Tensor | None:
     if split_k <= 1:
         return None
     rows = q.shape[0] * (q.shape[1] if q.dim() == 4 else 1)
-    n = _hip.decode_counters_bytes(rows, q.shape[-2]) // 4
+    n = rows * q.shape[-2]  # fat_paged_decode_counters_bytes / 4: one int32 per (query row, head)
     key = (q.device.index if q.device.index is not None else torch.cuda.current_device(),
            _hip.current_stream_handle(q.device))
     t = _MERGE_COUNTERS.get(key)
@@ -263,8 +263,8 @@ def paged_decode_launch(
     if scales is not None:
         k_scale = scales["k"] if isinstance(scales, dict) else scales.k
         v_scale = scales["v"] if isinstance(scales, dict) else scales.v
-    if counters is not None and counters.numel() * counters.element_size() < _hip.decode_counters_bytes(
-            rows, q.shape[-2]):
+    # fat_paged_decode_counters_bytes: one int32 per (query row, head)
+    if counters is not None and counters.numel() * counters.element_size() < 4 * rows * q.shape[-2]:
         raise ValueError("paged_decode_launch: counters smaller than decode_counters_bytes(rows, num_heads)")
     _hip.paged_decode(q, cache.k_cache, cache.v_cache, pt, sl, out,
                       cache.page_size, softmax_scale, split_k, workspace=workspace,

@@ -44,6 +44,10 @@ def test_abi_version_and_workspace_sizes():
     assert _hip.decode_workspace_bytes(32, 32, 128, 1) == 0
     assert _hip.decode_workspace_bytes(32, 32, 128, 4) == 32 * 32 * 4 * 130 * 4
     assert _hip.prefill_workspace_bytes(1, 1, 128) >= 0
+    # one int32 counter per (query row, head); the Python wrappers size
+    # their cached counter buffers with this formula
+    for rows, heads in ((0, 32), (1, 1), (32, 32), (128 * 4, 8)):
+        assert _hip.decode_counters_bytes(rows, heads) == 4 * rows * heads
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
