@@ -21,13 +21,15 @@ Shapes (synthetic, seeded, N(0, 1) values, randomly permuted page pools):
 decode fp16 32/8 heads D128 P16 for B in {1, 8, 32, 128} x ctx in {128,
 1024, 4096, 16384}; int8 and fp8 decode B128 ctx16384; B1 ctx131072; MQA
 32/1 B32 ctx4096; 4-token decode B32 ctx4096; bf16 and D64 decode B32
-ctx4096; causal prefill of one fp16
+ctx4096; the skewed batch of 64 log-uniform lengths in [16, 65536] (the
+benchmark's own draw); causal prefill of one fp16
 sequence, L in {512, ..., 8192}; paged prefill L8192 at page size 16.
 """
 
 from __future__ import annotations
 
 import argparse
+import math
 import json
 import statistics
 import sys
@@ -55,6 +57,37 @@ DECODE_SHAPES = [(b, ctx, 32, 8, None, 1) for b in (1, 8, 32, 128) for ctx in (1
 ]
 PREFILL_LENS = (512, 1024, 2048, 4096, 8192)
 D, P = 128, 16
+
+
+def skewed_lens() -> list[int]:
+    """The long-context stress config's skewed batch, as
+    ``bench.py --all-configs`` draws it: 64 log-uniform lengths in [16, 65536]
+    (seed 64)."""
+    g = torch.Generator().manual_seed(64)
+    logs = torch.rand(64, generator=g) * (math.log(65536) - math.log(16)) + math.log(16)
+    return [int(math.exp(x)) for x in logs.tolist()]
+
+
+# the skewed batch: (batch, "skewed", query heads, KV heads, quantised dtype, q_len)
+DECODE_SHAPES.append((64, "skewed", 32, 8, None, 1))
+
+
+def _ragged_cache(lens: list[int], hkv: int, gen: torch.Generator, device, d: int = D,
+                  dtype=torch.float16) -> PagedKVCache:
+    """A paged cache holding sequences of the given lengths, pages randomly
+    permuted over one pool."""
+    per = [-(-n // P) for n in lens]
+    num_pages = sum(per)
+    perm = torch.randperm(num_pages, generator=gen, device=device).to(torch.int32)
+    table = torch.zeros(len(lens), max(per), dtype=torch.int32, device=device)
+    at = 0
+    for b, n in enumerate(per):
+        table[b, :n] = perm[at:at + n]
+        at += n
+    k = torch.randn(num_pages, P, hkv, d, generator=gen, device=device, dtype=torch.float32).to(dtype)
+    v = torch.randn(num_pages, P, hkv, d, generator=gen, device=device, dtype=torch.float32).to(dtype)
+    return PagedKVCache(k_cache=k, v_cache=v, page_table=table,
+                        seq_lens=torch.tensor(lens, dtype=torch.int32, device=device), page_size=P)
 
 
 def _paged_cache(batch: int, ctx: int, hkv: int, gen: torch.Generator, device, d: int = D,
@@ -103,11 +136,13 @@ def tune_decode(device, out_path, min_gain: float) -> None:
     for shape in DECODE_SHAPES:
         batch, ctx, hq, hkv, qdt, q_len = shape[:6]
         d, dtype = shape[6:] if len(shape) > 6 else (D, torch.float16)
-        gen = torch.Generator(device=device).manual_seed(batch * 7919 + ctx)
-        pool_bytes = batch * ctx * hkv * d * 2 * (1 if qdt is not None else 2)
+        lens = skewed_lens() if ctx == "skewed" else [ctx] * batch
+        gen = torch.Generator(device=device).manual_seed(batch * 7919 + max(lens))
+        pool_bytes = sum(lens) * hkv * d * 2 * (1 if qdt is not None else 2)
         caches, scale_list = [], []
         for _ in range(_copies(pool_bytes)):
-            cache = _paged_cache(batch, ctx, hkv, gen, device, d, dtype)
+            cache = (_ragged_cache(lens, hkv, gen, device, d, dtype) if ctx == "skewed"
+                     else _paged_cache(batch, ctx, hkv, gen, device, d, dtype))
             scales = None
             if qdt is not None:
                 cache, scales = quantize_cache(cache, "int8" if qdt == torch.int8 else "fp8")
@@ -118,8 +153,8 @@ def tune_decode(device, out_path, min_gain: float) -> None:
         q = torch.randn(*qshape, generator=gen, device=device, dtype=torch.float32).to(dtype)
         out = torch.empty_like(q)
         ws = torch.empty(_hip.decode_workspace_bytes(batch * q_len, hq, d, 64), dtype=torch.uint8, device=device)
-        max_pages = -(-ctx // P)
-        total = batch * max_pages
+        max_pages = -(-max(lens) // P)
+        total = sum(-(-n // P) for n in lens)
         quantized = qdt is not None
         split, pps = decode_partition(batch, hq, hkv, max_pages, total, quantized=quantized, q_len=q_len)
         default = {"split_k": split, "pages_per_split": pps, "num_warps": None, "kernel": None}
@@ -135,11 +170,11 @@ def tune_decode(device, out_path, min_gain: float) -> None:
                                 pages_per_split=cfg["pages_per_split"], kernel=cfg["kernel"],
                                 counters=merge_counters(q, cfg["split_k"]))
 
-        nbytes = bytes_decode_paged([ctx] * batch, hq * q_len, hkv, d, kv_elem_bytes=1 if quantized else 2,
+        nbytes = bytes_decode_paged(lens, hq * q_len, hkv, d, kv_elem_bytes=1 if quantized else 2,
                                     page_size=P, quantized=quantized)
-        sig = decode_signature(batch, hq, hkv, d, P, ctx, total, cache.k_cache.dtype, q_len)
+        sig = decode_signature(batch, hq, hkv, d, P, max(lens), total, cache.k_cache.dtype, q_len)
         problem = {"kind": "decode", "signature": sig, "runner": run, "bytes": nbytes,
-                   "flops": 4 * batch * hq * q_len * d * ctx}
+                   "flops": 4 * hq * q_len * d * sum(lens)}
         rows = autotune(problem, cands, save=False, timer=_timer)
         cfg, metrics = _pick(problem, rows, default, list(default), min_gain)
         save_best("decode", sig, cfg, metrics, path=out_path)

@@ -143,12 +143,16 @@ def test_committed_decode_entry_at_full_size(sig):
     assert m, sig
     B, H, HKV, D, P, L = (int(m.group(i)) for i in range(1, 7))
     tag, T = m.group(7), int(m.group(8) or 1)
-    assert not m.group(9), "ragged store entries are not generated here"
+    seq = [L] * B
+    if m.group(9):  # ragged: the tuner's only ragged shape is the skewed benchmark batch
+        from flashattntile_amd.tune import skewed_lens
+        seq = skewed_lens()
+        assert (B, L) == (len(seq), max(seq)), f"{sig}: not the tuner's skewed batch"
     label = f"store decode {sig}"
     print(label, flush=True)
     stored = at.best_config("decode", sig)
-    table, num_pages = _table([L] * B, P, seed=B + L)
-    lens = torch.full((B,), L, dtype=torch.int32)
+    table, num_pages = _table(seq, P, seed=B + L)
+    lens = torch.tensor(seq, dtype=torch.int32)
     qdtype = torch.bfloat16 if tag == "bf16" else torch.float16
     g = torch.Generator().manual_seed(L + H)
     shape = (B, T, H, D) if T > 1 else (B, H, D)
