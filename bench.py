@@ -975,9 +975,8 @@ def all_configs(args, device):
     emit(_decode_row("decode fp16 B1 ctx131072 split16", [131072], 32, 8, 128, 16, device, args, flush, split=16,
                      cpu_seqs=1))
     emit(_decode_row("decode fp16 B1 ctx131072", [131072], 32, 8, 128, 16, device, args, flush, cpu_seqs=1))
-    g = torch.Generator().manual_seed(64)
-    skew = [int(math.exp(x)) for x in (torch.rand(64, generator=g) * (math.log(65536) - math.log(16))
-                                       + math.log(16)).tolist()]
+    from flashattntile_amd.tune import skewed_lens  # the tuner's draw, so its store entry matches
+    skew = skewed_lens()
     emit(_decode_row(f"decode fp16 skewed64 sum{sum(skew)}", skew, 32, 8, 128, 16, device, args, flush))
     emit(_decode_row("decode fp16 MQA 32/1 B32 ctx4096", [4096] * 32, 32, 1, 128, 16, device, args, flush))
     emit(_decode_row("decode fp16 D64 B32 ctx4096", [4096] * 32, 32, 8, 64, 16, device, args, flush))
